@@ -1,0 +1,321 @@
+#!/usr/bin/env python3
+"""Benchmark of the sliding-window + sink FlashAttention-2 hot path on one MI355X.
+
+A step is one forward + backward of the attention layer through the drop-in boundary
+(flash_swda_with_sink, then o.backward(dO)) on synthetic, seeded inputs already resident in HBM.
+The default workload is BASELINE config c2 (GPT-OSS sliding-window layer: B=1, Hq=64, Hkv=8,
+L=4096, D=64, W=128, S=4, bf16).  Protocol after the reference's timers
+(benchmark_backward_speed.py:720-783): W warm-up steps, then K timed steps bracketed by
+torch.cuda.synchronize() and wall-clock perf_counter; forward-only and backward-only are timed the
+same way.  Prints ONE JSON line.
+
+  value        effective TFLOP/s of fwd+bwd, counting only allowed (unmasked) score pairs
+               (14*D FLOPs per pair per head), whole job
+  ms_per_step  fwd+bwd milliseconds
+  roofline     the dominant kernel: algorithmic bytes (or FLOPs) per launch / its average
+               duration measured with HIP events on the launch stream
+  cpu_baseline the reference's naive PyTorch path (oracle/naive.py, in the config dtype) timed
+               on the host cores on a bounded sample (whole KV groups of the same workload)
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "fwd+bwd ms & effective TFLOP/s (unmasked FLOPs), Hq64/Hkv8 D64 W128 bf16"
+
+CONFIGS = {
+    "c1": dict(B=1, Hq=16, Hkv=16, L=4096, D=16, W=256, S=4, dtype="fp16", do_std=1.0,
+               name="README benchmark shape"),
+    "c2": dict(B=1, Hq=64, Hkv=8, L=4096, D=64, W=128, S=4, dtype="bf16", do_std=1.0,
+               name="GPT-OSS sliding-window attention layer"),
+    "c3": dict(B=1, Hq=64, Hkv=8, L=8192, D=64, W=8192, S=0, dtype="bf16", do_std=1.0,
+               name="GPT-OSS full-causal layer"),
+    "c4": dict(B=1, Hq=64, Hkv=8, L=32768, D=64, W=128, S=4, dtype="bf16", do_std=0.1,
+               name="long-context window layer"),
+    "c5": dict(B=8, Hq=32, Hkv=4, L=2048, D=128, W=512, S=16, dtype="fp16", do_std=1.0,
+               name="batched wide-head variant"),
+}
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0
+
+
+def _pkg():
+    return importlib.import_module("flashattention-gpt-oss-finetuning_amd")
+
+
+def _mod(name):
+    return importlib.import_module("flashattention-gpt-oss-finetuning_amd." + name)
+
+
+def make_inputs(cfg, device, seed=0):
+    import torch
+
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16}[cfg["dtype"]]
+    g = torch.Generator().manual_seed(seed)
+    B, Hq, Hkv, L, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"], cfg["D"]
+    q = torch.randn(B, Hq, L, D, generator=g)
+    k = torch.randn(B, Hkv, L, D, generator=g)
+    v = torch.randn(B, Hkv, L, D, generator=g)
+    do = torch.randn(B, Hq, L, D, generator=g) * cfg["do_std"]
+    return [t.to(dt).to(device) for t in (q, k, v, do)]
+
+
+def kernel_accounting(cfg):
+    """Algorithmic FLOPs and bytes of each kernel launch (allowed pairs only; each tensor moved once)."""
+    flops_mod = _mod("flops")
+    B, Hq, Hkv, L, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"], cfg["D"]
+    pairs = flops_mod.allowed_pairs_per_head(L, cfg["W"], cfg["S"])
+    qb = B * Hq * L * D * 2
+    kvb = B * Hkv * L * D * 2
+    rowb = B * Hq * L * 4
+    per = lambda n: float(n) * D * pairs * B * Hq
+    return {
+        # forward: QK^T, PV; reads Q K V, writes O and LSE
+        "fwd": dict(flops=per(4), bytes=float(qb + 2 * kvb + qb + rowb)),
+        # dQ: QK^T, dO V^T, dS K; reads Q K V O dO LSE, writes dQ and delta
+        "bwd_dq": dict(flops=per(6), bytes=float(4 * qb + 2 * kvb + 2 * rowb)),
+        # dK/dV: QK^T, dO V^T, P^T dO, dS^T Q; reads Q dO K V LSE delta, writes dK dV
+        "bwd_dkdv": dict(flops=per(8), bytes=float(2 * qb + 4 * kvb + 2 * rowb)),
+    }
+
+
+def time_kernels(cfg, q, k, v, do, iters=50):
+    """Average duration of each kernel, launched alone through the C ABI, measured with HIP events
+    recorded on the stream the kernel is launched on (torch's current stream)."""
+    import torch
+
+    ops = _mod("_ops")
+    scale = 1.0 / math.sqrt(cfg["D"])
+    fc = ops.FwdCall(q, k, v, cfg["W"], cfg["S"], scale)
+    fc.run()
+    bc = ops.BwdCall(q, k, v, fc.o, fc.lse, do, cfg["W"], cfg["S"], scale)
+    bc.run()
+    stages = {"fwd": fc.run, "bwd_dq": lambda: bc.run("dq"), "bwd_dkdv": lambda: bc.run("dkdv")}
+    out = {}
+    stream = torch.cuda.current_stream()
+    for name, fn in stages.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(iters):
+            fn()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        out[name] = t0.elapsed_time(t1) / iters * 1e3  # microseconds
+    return out
+
+
+def time_steps(fa, cfg, q, k, v, do, steps, warmup):
+    import torch
+
+    qg, kg, vg = (t.detach().clone().requires_grad_() for t in (q, k, v))
+    W, S = cfg["W"], cfg["S"]
+
+    def step():
+        qg.grad = kg.grad = vg.grad = None
+        o = fa.flash_swda_with_sink(qg, kg, vg, W, S)
+        o.backward(do)
+
+    # forward + backward
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    fb_ms = (time.perf_counter() - t0) * 1e3 / steps
+    fb_event_ms = ev0.elapsed_time(ev1) / steps
+    peak_gb = torch.cuda.max_memory_allocated() / 2 ** 30
+
+    # forward only (no autograd graph)
+    with torch.no_grad():
+        for _ in range(warmup):
+            fa.flash_swda_with_sink(q, k, v, W, S)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fa.flash_swda_with_sink(q, k, v, W, S)
+        torch.cuda.synchronize()
+        f_ms = (time.perf_counter() - t0) * 1e3 / steps
+
+    # backward only: forward, sync, then time backward (benchmark_backward_speed.py:761-783)
+    total = 0.0
+    for i in range(warmup + steps):
+        qg.grad = kg.grad = vg.grad = None
+        o = fa.flash_swda_with_sink(qg, kg, vg, W, S)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        o.backward(do)
+        torch.cuda.synchronize()
+        if i >= warmup:
+            total += time.perf_counter() - t0
+    b_ms = total * 1e3 / steps
+    return dict(fwdbwd_ms=fb_ms, fwdbwd_event_ms=fb_event_ms, fwd_ms=f_ms, bwd_ms=b_ms, peak_mem_gb=peak_gb)
+
+
+def cpu_baseline(cfg, budget_s):
+    """The reference's naive path (benchmark_backward_speed.py:68-85, restated in oracle/naive.py)
+    in the config dtype on the host cores, forward + autograd backward, on whole KV groups of the
+    same workload until `budget_s` seconds have been spent (at least one group)."""
+    import torch
+
+    from oracle import naive  # the CPU baseline leg
+
+    flops_mod = _mod("flops")
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16}[cfg["dtype"]]
+    B, Hq, Hkv, L, D, W, S = (cfg[x] for x in ("B", "Hq", "Hkv", "L", "D", "W", "S"))
+    G = Hq // Hkv
+    q, k, v, do = make_inputs(cfg, "cpu")
+    # warm up the thread pool and allocator on one head of a short prefix
+    qw = q[:1, :1, :256].clone().requires_grad_()
+    ow = naive.naive_attention(qw, k[:1, :1, :256], v[:1, :1, :256], W, S)
+    ow.backward(do[:1, :1, :256])
+    groups = 0
+    t0 = time.perf_counter()
+    elapsed = 0.0
+    for b in range(B):
+        for g in range(Hkv):
+            qs = q[b:b + 1, g * G:(g + 1) * G].clone().requires_grad_()
+            ks = k[b:b + 1, g:g + 1].clone().requires_grad_()
+            vs = v[b:b + 1, g:g + 1].clone().requires_grad_()
+            o = naive.naive_attention(qs, ks, vs, W, S)
+            o.backward(do[b:b + 1, g * G:(g + 1) * G])
+            groups += 1
+            elapsed = time.perf_counter() - t0
+            if elapsed >= budget_s:
+                break
+        if elapsed >= budget_s:
+            break
+    pairs = flops_mod.allowed_pairs_per_head(L, W, S)
+    flops = 14.0 * D * pairs * groups * G
+    total_groups = B * Hkv
+    return {
+        "value": flops / elapsed / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{groups} of {total_groups} KV groups ({groups * G} of {B * Hq} query heads) of the same "
+                  f"workload, fwd+bwd of the naive path in {cfg['dtype']} (dense scores, fp32 softmax, autograd), "
+                  f"{elapsed:.1f} s; full-workload estimate {elapsed * total_groups / groups * 1e3:.0f} ms",
+        "ms_full_workload_est": elapsed * total_groups / groups * 1e3,
+        "cpu": platform.processor() or platform.machine(),
+        "logical_cores": os.cpu_count(),
+        "torch_threads": torch.get_num_threads(),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--cpu-baseline-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--table", action="store_true", help="also time every BASELINE config (stderr)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE={world}); this build has no "
+              "multi-GPU path: attention shards with zero communication over batch and KV-head groups, so the "
+              "per-GPU kernel is what --gpus 1 measures.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    fa = _pkg()
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    q, k, v, do = make_inputs(cfg, dev)
+    acct = kernel_accounting(cfg)
+    wl = _mod("flops").Workload(cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"], cfg["D"], cfg["W"], cfg["S"])
+
+    t = time_steps(fa, cfg, q, k, v, do, args.steps, args.warmup)
+    kus = time_kernels(cfg, q, k, v, do, iters=args.kernel_iters)
+
+    kernels = {}
+    for name, us in kus.items():
+        a = acct[name]
+        ai = a["flops"] / a["bytes"]
+        kernels[name] = dict(avg_us=round(us, 3), alg_bytes=a["bytes"], useful_flops=a["flops"],
+                             gbs=round(a["bytes"] / us / 1e3, 1), tflops=round(a["flops"] / us / 1e6, 1),
+                             bound="hbm" if ai < MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma")
+    dom = max(kernels, key=lambda n: kernels[n]["avg_us"])
+    dk = kernels[dom]
+    if dk["bound"] == "hbm":
+        achieved, peak, unit = dk["gbs"], HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, unit = dk["tflops"], MFMA_PEAK_TFLOPS, "TFLOP/s"
+    roofline = {"kernel": dom, "bound": dk["bound"], "achieved": achieved, "peak": peak, "unit": unit,
+                "frac": round(achieved / peak, 4), "traffic": None, "avg_us": dk["avg_us"]}
+
+    fb_flops = wl.flops("fwdbwd")
+    value = fb_flops / (t["fwdbwd_ms"] * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t["fwdbwd_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg["dtype"],
+        "data": "synthetic (seeded N(0,1) q, k, v, dO)",
+        "config": {"workload": f"{args.config}: {cfg['name']}, fwd+bwd", "batch": cfg["B"], "heads_q": cfg["Hq"],
+                   "heads_kv": cfg["Hkv"], "seq_len": cfg["L"], "head_dim": cfg["D"], "window": cfg["W"],
+                   "sink": cfg["S"], "parallelism": "single GPU"},
+        "fwd_ms": round(t["fwd_ms"], 4),
+        "bwd_ms": round(t["bwd_ms"], 4),
+        "fwdbwd_event_ms": round(t["fwdbwd_event_ms"], 4),
+        "peak_mem_gb": round(t["peak_mem_gb"], 4),
+        "fwdbwd_roofline_frac": round(wl.roofline_seconds("fwdbwd") / (t["fwdbwd_ms"] * 1e-3), 4),
+        "kernels": kernels,
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_baseline_seconds)
+    if args.table:
+        for name, c in CONFIGS.items():
+            qq, kk, vv, dd = make_inputs(c, dev)
+            tt = time_steps(fa, c, qq, kk, vv, dd, args.steps, args.warmup)
+            w = _mod("flops").Workload(c["B"], c["Hq"], c["Hkv"], c["L"], c["D"], c["W"], c["S"])
+            print(json.dumps({"config": name, **{k_: round(v_, 4) for k_, v_ in tt.items()},
+                              "tflops": round(w.flops("fwdbwd") / (tt["fwdbwd_ms"] * 1e-3) / 1e12, 2),
+                              "roofline_frac": round(w.roofline_seconds("fwdbwd") / (tt["fwdbwd_ms"] * 1e-3), 4)}),
+                  file=sys.stderr, flush=True)
+            del qq, kk, vv, dd
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

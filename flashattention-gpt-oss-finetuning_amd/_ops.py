@@ -1,0 +1,176 @@
+"""Tensor-level calls into libfa_gfx950.so: argument marshalling, output allocation, streams.
+
+PyTorch provides device memory (the caching allocator) and the current HIP stream; every
+FLOP runs in the library's HIP kernels.  Inputs the kernels cannot read directly (head-dim
+stride != 1, rows not 16-byte aligned) are first copied to a contiguous layout, as the
+reference benchmark does for dO (benchmark_backward_speed.py:510).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.bfloat16: _lib.FA_DTYPE_BF16, torch.float16: _lib.FA_DTYPE_F16}
+_I32_MIN, _I32_MAX = -(2 ** 31), 2 ** 31 - 1
+
+
+def _i32(x: int) -> int:
+    return _I32_MIN if x < _I32_MIN else (_I32_MAX if x > _I32_MAX else x)
+
+
+def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+    st = t.stride()
+    if st[3] != 1 or (t.data_ptr() & 15) or (st[0] & 7) or (st[1] & 7) or (st[2] & 7):
+        t = t.contiguous()
+        if t.data_ptr() & 15:
+            t = t.clone(memory_format=torch.contiguous_format)
+    return t
+
+
+def _check(tensors, names):
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(
+            f"{names[0]} is on {dev}: the gfx950 attention kernels need GPU tensors "
+            "(there is no CPU implementation)"
+        )
+    dt = tensors[0].dtype
+    if dt not in _DTYPES:
+        raise ValueError(f"{names[0]} has dtype {dt}; supported dtypes are bfloat16 and float16")
+    for t, n in zip(tensors, names):
+        if t.dim() != 4:
+            raise ValueError(f"{n} must be 4-D [B, H, L, D], got shape {tuple(t.shape)}")
+        if t.device != dev:
+            raise RuntimeError(f"{n} is on {t.device} but {names[0]} is on {dev}")
+        if t.dtype != dt:
+            raise ValueError(f"{n} has dtype {t.dtype} but {names[0]} has {dt}")
+
+
+def _strides3(t: torch.Tensor):
+    s = t.stride()
+    return (s[0], s[1], s[2])
+
+
+class _DeviceGuard:
+    """Makes `device` current for the HIP launch when it is not already (cheap no-op otherwise)."""
+
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, device: torch.device):
+        self.idx = device.index if device.index is not None else torch.cuda.current_device()
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.idx:
+            self.prev = cur
+            torch.cuda.set_device(self.idx)
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+class FwdCall:
+    """A prepared forward launch: validated inputs, allocated outputs and a filled parameter
+    block.  ``run()`` launches on the current stream of the inputs' device."""
+
+    __slots__ = ("params", "inputs", "o", "lse", "device")
+
+    def __init__(self, q, k, v, window: int, sink: int, scale: float):
+        _check((q, k, v), ("q", "k", "v"))
+        q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+        B, Hq, L, D = q.shape
+        Hkv = k.shape[1]
+        self.o = torch.empty((B, Hq, L, D), dtype=q.dtype, device=q.device)
+        self.lse = torch.empty((B, Hq, L), dtype=torch.float32, device=q.device)
+        self.inputs = (q, k, v)  # keeps the (possibly copied) inputs alive
+        self.device = q.device
+        p = _lib.FwdParams()
+        p.q, p.k, p.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+        p.o, p.lse = self.o.data_ptr(), self.lse.data_ptr()
+        p.q_stride[:] = _strides3(q)
+        p.k_stride[:] = _strides3(k)
+        p.v_stride[:] = _strides3(v)
+        p.o_stride[:] = _strides3(self.o)
+        p.lse_stride[:] = self.lse.stride()
+        p.batch, p.heads_q, p.heads_kv, p.seqlen, p.head_dim = B, Hq, Hkv, L, D
+        p.window, p.sink = _i32(window), _i32(sink)
+        p.softmax_scale = scale
+        p.dtype = _DTYPES[q.dtype]
+        self.params = p
+
+    def run(self) -> None:
+        with _DeviceGuard(self.device):
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            rc = _lib.lib().fa_fwd(ctypes.byref(self.params), ctypes.c_void_p(stream))
+        _lib.raise_for_status(rc, "fa_fwd")
+
+
+def forward(q, k, v, window: int, sink: int, scale: float):
+    """Returns (o, lse) for q [B,Hq,L,D], k/v [B,Hkv,L,D]."""
+    call = FwdCall(q, k, v, window, sink, scale)
+    call.run()
+    return call.o, call.lse
+
+
+def workspace_bytes(B, Hq, Hkv, L, D, window, sink) -> int:
+    return int(_lib.lib().fa_bwd_workspace_bytes(B, Hq, Hkv, L, D, _i32(window), _i32(sink)))
+
+
+class BwdCall:
+    """A prepared backward launch (outputs dq, dk, dv and the workspace allocated once).
+    ``run(stage)`` launches fa_bwd ("all"), fa_bwd_dq ("dq") or fa_bwd_dkdv ("dkdv")."""
+
+    __slots__ = ("params", "inputs", "dq", "dk", "dv", "ws", "device")
+
+    def __init__(self, q, k, v, o, lse, do, window: int, sink: int, scale: float):
+        _check((q, k, v, o, do), ("q", "k", "v", "o", "do"))
+        q, k, v, o, do = (_kernel_ready(t) for t in (q, k, v, o, do))
+        B, Hq, L, D = q.shape
+        Hkv = k.shape[1]
+        dev = q.device
+        self.dq = torch.empty((B, Hq, L, D), dtype=q.dtype, device=dev)
+        self.dk = torch.empty((B, Hkv, L, D), dtype=k.dtype, device=dev)
+        self.dv = torch.empty((B, Hkv, L, D), dtype=v.dtype, device=dev)
+        ws_bytes = workspace_bytes(B, Hq, Hkv, L, D, window, sink)
+        self.ws = torch.empty((max(ws_bytes, 256),), dtype=torch.uint8, device=dev)
+        self.inputs = (q, k, v, o, lse, do)
+        self.device = dev
+        p = _lib.BwdParams()
+        p.q, p.k, p.v, p.o, p.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr()
+        p.lse = lse.data_ptr()
+        p.dq, p.dk, p.dv = self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr()
+        p.q_stride[:] = _strides3(q)
+        p.k_stride[:] = _strides3(k)
+        p.v_stride[:] = _strides3(v)
+        p.o_stride[:] = _strides3(o)
+        p.do_stride[:] = _strides3(do)
+        p.lse_stride[:] = lse.stride()
+        p.dq_stride[:] = _strides3(self.dq)
+        p.dk_stride[:] = _strides3(self.dk)
+        p.dv_stride[:] = _strides3(self.dv)
+        p.batch, p.heads_q, p.heads_kv, p.seqlen, p.head_dim = B, Hq, Hkv, L, D
+        p.window, p.sink = _i32(window), _i32(sink)
+        p.softmax_scale = scale
+        p.dtype = _DTYPES[q.dtype]
+        self.params = p
+
+    def run(self, stage: str = "all") -> None:
+        fn = {"all": "fa_bwd", "dq": "fa_bwd_dq", "dkdv": "fa_bwd_dkdv"}[stage]
+        with _DeviceGuard(self.device):
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            rc = getattr(_lib.lib(), fn)(ctypes.byref(self.params), ctypes.c_void_p(self.ws.data_ptr()),
+                                         ctypes.c_size_t(self.ws.numel()), ctypes.c_void_p(stream))
+        _lib.raise_for_status(rc, fn)
+
+
+def backward(q, k, v, o, lse, do, window: int, sink: int, scale: float):
+    """Returns (dq, dk, dv) in the input dtype."""
+    call = BwdCall(q, k, v, o, lse, do, window, sink, scale)
+    call.run()
+    return call.dq, call.dk, call.dv

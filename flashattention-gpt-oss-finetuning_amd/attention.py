@@ -1,0 +1,73 @@
+"""Drop-in replacement for the reference's autograd boundary.
+
+``FlashSWDAWithSink`` and ``flash_swda_with_sink`` keep the calling surface of
+flash_attention_gpt_oss.py:340-438 (same names, argument order, defaults, assertion messages,
+saved tensors and 7-tuple of gradients); ``swa_sink_attention`` has the
+``func(q, k, v, window_size, sink_size) -> o`` form of the benchmark's registries
+(benchmark_backward_speed.py:615-643).  Compute goes to libfa_gfx950.so through :mod:`._ops`;
+there is no CPU or PyTorch fallback: tensors that are not on a GPU raise.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _ops
+
+
+class FlashSWDAWithSink(torch.autograd.Function):
+    """Causal GQA attention with a sliding window and positional sink keys.
+
+    forward(q [B,Hq,L,D], k [B,Hkv,L,D], v [B,Hkv,L,D], window_size, sink_size,
+            is_causal=True, softmax_scale=None) -> o [B,Hq,L,D]
+    (flash_attention_gpt_oss.py:341-385).  Saves (q, k, v, o, lse) for backward; lse is the
+    natural-log log-sum-exp per query row, float32 [B,Hq,L].
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, window_size, sink_size, is_causal=True, softmax_scale=None):
+        # Checks of flash_attention_gpt_oss.py:343-354, same conditions and messages.
+        if not is_causal:
+            raise AssertionError("Currently, only causal attention is supported")
+        if softmax_scale is None:
+            softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+        batch, n_q_heads, seq_len, head_dim = q.shape
+        _, n_kv_heads, _, _ = k.shape
+        if not (q.shape[0] == v.shape[0] and q.shape[2] == v.shape[2] and q.shape[3] == v.shape[3]):
+            raise AssertionError("Query and Value shapes must be compatible except for num_heads")
+        if not (k.shape[0] == v.shape[0] and k.shape[1] == v.shape[1] and k.shape[2] == v.shape[2]
+                and k.shape[3] == v.shape[3]):
+            raise AssertionError("Key and Value shapes must be the same")
+        if not head_dim <= 128:
+            raise AssertionError("Head dimension must be less than or equal to 128")
+        if not n_q_heads % n_kv_heads == 0:
+            raise AssertionError("Number of query heads must be divisible by number of K/V heads")
+
+        o, lse = _ops.forward(q, k, v, int(window_size), int(sink_size), float(softmax_scale))
+
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.softmax_scale = softmax_scale
+        ctx.window_size = window_size
+        ctx.sink_size = sink_size
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = _ops.backward(q, k, v, o, lse, do, int(ctx.window_size), int(ctx.sink_size),
+                                   float(ctx.softmax_scale))
+        return dq, dk, dv, None, None, None, None
+
+
+def flash_swda_with_sink(q, k, v, window_size: int, sink_size: int = 0, is_causal: bool = True,
+                         scale: Optional[float] = None):
+    """Functional form, flash_attention_gpt_oss.py:437-438."""
+    return FlashSWDAWithSink.apply(q, k, v, window_size, sink_size, is_causal, scale)
+
+
+def swa_sink_attention(q, k, v, window_size: int, sink_size: int):
+    """Registry form ``func(q, k, v, window_size, sink_size) -> o`` with the default scale 1/sqrt(D)
+    (benchmark_backward_speed.py:615-643)."""
+    return FlashSWDAWithSink.apply(q, k, v, window_size, sink_size, True, None)

@@ -1,0 +1,51 @@
+// fa_args.h - kernel argument block shared by the C ABI (fa_capi.cpp) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+// Everything a kernel needs, passed by value through the kernarg segment.  Strides are in
+// elements; sequence indices are int32 (validated: L < 2^28), offsets are formed in int64.
+struct Args {
+  // inputs
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;     // backward: forward output
+  const void* dout;  // backward: upstream gradient
+  const float* lse;  // backward: forward statistic
+  // outputs
+  void* o_out;       // forward
+  float* lse_out;    // forward
+  void* dq;
+  void* dk;
+  void* dv;
+  // backward workspace
+  float* delta;      // [B][Hq][Lp] fp32, Lp = L rounded up to 32
+  float* partial;    // sink-key partial sums, see fa_bwd.hip
+  int64_t sq[3], sk[3], sv[3], so[3], sdo[3], slse[3], sdq[3], sdk[3], sdv[3], so_out[3];
+  int B, Hq, Hkv, L, G, Lp;
+  int W, S;          // window and sink, clamped to [0, L]
+  float scale;       // softmax scale as given
+  float c;           // |scale| * log2(e), kept > 0: scores enter exp2 as s * c
+  uint32_t qsign;    // 0x80008000 when scale < 0: flips the sign of Q in the score product
+  // q-major kernels (forward, dQ): a workgroup is wq x wh waves, each wave 32 rows x HPW heads
+  int wq, wh;
+  int n_qtiles;
+  // KV-major kernel (dK/dV)
+  int n_kblocks;     // ceil(L / 32)
+  int nsp;           // leading 32-key blocks whose sink rows are split into chunks
+  int n_chunks;      // chunks of chunk_rows query rows (0 when nsp == 0)
+  int chunk_rows;
+  int n_chunk_wgs;   // B * Hkv * nsp * n_chunks
+};
+
+// Launchers (return the hipError_t of the launch).
+hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
+hipError_t launch_bwd_dq(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
+hipError_t launch_bwd_dkdv(const Args& a, int dtype, int D, hipStream_t stream);
+hipError_t launch_bwd_sink_finalize(const Args& a, int dtype, int D, hipStream_t stream);
+
+}  // namespace fa

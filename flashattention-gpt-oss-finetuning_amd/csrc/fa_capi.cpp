@@ -1,0 +1,293 @@
+// fa_capi.cpp - the C ABI declared in include/fa_gfx950.h: host-side validation, workspace
+// sizing, launch-shape selection and dispatch to the gfx950 kernels.
+//
+// Validation mirrors the reference's checks (flash_attention_gpt_oss.py:343-354:
+// causal only, shape agreement, D <= 128, Hq % Hkv == 0; benchmark_backward_speed.py:476-484)
+// plus what the kernels assume (16-byte aligned rows, D in {16, 32, 64, 128}).  Nothing in
+// fa_check_* touches HIP, so the checks run on machines without a GPU.
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+
+#include "../../include/fa_gfx950.h"
+#include "fa_args.h"
+#include "fa_plan.h"
+
+namespace {
+
+constexpr int64_t kMaxSeq = int64_t(1) << 28;
+constexpr int kChunkRows = 256;  // query rows per sink-chunk workgroup of the dK/dV kernel
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool strides_ok(const int64_t s[3]) {
+  for (int i = 0; i < 3; ++i)
+    if (s[i] < 0 || (s[i] & 7) != 0) return false;
+  return true;
+}
+
+bool lse_strides_ok(const int64_t s[3]) { return s[0] >= 0 && s[1] >= 0 && s[2] >= 0; }
+
+bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+int check_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t L, int32_t D, int32_t W, int32_t S,
+                 float scale, int32_t dtype) {
+  if (B < 1 || Hq < 1 || Hkv < 1 || L < 1) return FA_ERR_SHAPE;
+  if (Hq % Hkv != 0) return FA_ERR_SHAPE;
+  if (D != 16 && D != 32 && D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+  if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F16) return FA_ERR_DTYPE;
+  if (W < 1 && S < 1) return FA_ERR_MASK;
+  if (!std::isfinite(scale)) return FA_ERR_SCALE;
+  if (int64_t(L) > kMaxSeq) return FA_ERR_OVERFLOW;
+  // grid sizes of the launches must fit 32 bits
+  if (int64_t(B) * Hq * ((int64_t(L) + 31) / 32) > (int64_t(1) << 31)) return FA_ERR_OVERFLOW;
+  return FA_OK;
+}
+
+// Workgroup shape of the query-major kernels: wq waves along the sequence x wh waves along the
+// heads, each wave 32 rows x hpw heads; hpw * wh heads must divide the group size so that a
+// workgroup never straddles two KV heads.
+void choose_qmajor(int G, int D, int* hpw, int* wh, int* wq) {
+  const int hmax = D <= 64 ? 2 : 1;
+  for (int h = hmax; h >= 1; --h)
+    for (int w = 4; w >= 1; w /= 2)
+      if (G % (h * w) == 0) {
+        *hpw = h;
+        *wh = w;
+        *wq = 4 / w;
+        return;
+      }
+  *hpw = 1;
+  *wh = 1;
+  *wq = 4;
+}
+
+struct SinkPlan {
+  int nsp, n_chunks;
+};
+
+SinkPlan sink_plan(int L, int W, int S) {
+  // clamp as the kernels do
+  W = W < 0 ? 0 : (W > L ? L : W);
+  S = S < 0 ? 0 : (S > L ? L : S);
+  SinkPlan p{0, 0};
+  p.nsp = fa::kv_sink_blocks(L, W, S);
+  if (p.nsp > 0) p.n_chunks = (L + kChunkRows - 1) / kChunkRows;
+  return p;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+size_t delta_bytes(int B, int Hq, int L) {
+  const size_t Lp = (size_t(L) + 31) / 32 * 32;
+  return align256(size_t(B) * Hq * Lp * sizeof(float));
+}
+
+size_t partial_bytes(int B, int Hkv, int D, const SinkPlan& sp) {
+  return align256(size_t(B) * Hkv * sp.nsp * (sp.n_chunks + 1) * 2 * 32 * D * sizeof(float));
+}
+
+void copy3(int64_t dst[3], const int64_t src[3]) {
+  for (int i = 0; i < 3; ++i) dst[i] = src[i];
+}
+
+fa::Args base_args(int32_t B, int32_t Hq, int32_t Hkv, int32_t L, int32_t D, int32_t W, int32_t S,
+                   float scale) {
+  fa::Args a;
+  std::memset(&a, 0, sizeof(a));
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.L = L;
+  a.G = Hq / Hkv;
+  a.Lp = (L + 31) / 32 * 32;
+  a.W = W < 0 ? 0 : (W > L ? L : W);
+  a.S = S < 0 ? 0 : (S > L ? L : S);
+  a.scale = scale;
+  float c = std::fabs(scale) * 1.4426950408889634f;
+  // A zero scale gives the uniform softmax; a tiny positive factor keeps -inf * c well defined
+  // and changes no fp32 result.
+  if (c < 1e-30f) c = 1e-30f;
+  a.c = c;
+  a.qsign = scale < 0.f ? 0x80008000u : 0u;
+  (void)D;
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_check_fwd(const fa_fwd_params* p) {
+  if (!p) return FA_ERR_NULL;
+  if (!p->q || !p->k || !p->v || !p->o || !p->lse) return FA_ERR_NULL;
+  const int rc = check_common(p->batch, p->heads_q, p->heads_kv, p->seqlen, p->head_dim, p->window,
+                              p->sink, p->softmax_scale, p->dtype);
+  if (rc != FA_OK) return rc;
+  if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o) || !aligned4(p->lse))
+    return FA_ERR_ALIGN;
+  if (!strides_ok(p->q_stride) || !strides_ok(p->k_stride) || !strides_ok(p->v_stride) ||
+      !strides_ok(p->o_stride) || !lse_strides_ok(p->lse_stride))
+    return FA_ERR_ALIGN;
+  return FA_OK;
+}
+
+int fa_check_bwd(const fa_bwd_params* p) {
+  if (!p) return FA_ERR_NULL;
+  if (!p->q || !p->k || !p->v || !p->o || !p->dout || !p->lse || !p->dq || !p->dk || !p->dv)
+    return FA_ERR_NULL;
+  const int rc = check_common(p->batch, p->heads_q, p->heads_kv, p->seqlen, p->head_dim, p->window,
+                              p->sink, p->softmax_scale, p->dtype);
+  if (rc != FA_OK) return rc;
+  const void* ptrs[] = {p->q, p->k, p->v, p->o, p->dout, p->dq, p->dk, p->dv};
+  for (const void* x : ptrs)
+    if (!aligned16(x)) return FA_ERR_ALIGN;
+  if (!aligned4(p->lse)) return FA_ERR_ALIGN;
+  if (!strides_ok(p->q_stride) || !strides_ok(p->k_stride) || !strides_ok(p->v_stride) ||
+      !strides_ok(p->o_stride) || !strides_ok(p->do_stride) || !lse_strides_ok(p->lse_stride) ||
+      !strides_ok(p->dq_stride) || !strides_ok(p->dk_stride) || !strides_ok(p->dv_stride))
+    return FA_ERR_ALIGN;
+  return FA_OK;
+}
+
+int fa_fwd(const fa_fwd_params* p, void* stream) {
+  const int rc = fa_check_fwd(p);
+  if (rc != FA_OK) return rc;
+  fa::Args a = base_args(p->batch, p->heads_q, p->heads_kv, p->seqlen, p->head_dim, p->window, p->sink,
+                         p->softmax_scale);
+  a.q = p->q;
+  a.k = p->k;
+  a.v = p->v;
+  a.o_out = p->o;
+  a.lse_out = p->lse;
+  copy3(a.sq, p->q_stride);
+  copy3(a.sk, p->k_stride);
+  copy3(a.sv, p->v_stride);
+  copy3(a.so_out, p->o_stride);
+  copy3(a.slse, p->lse_stride);
+  int hpw, wh, wq;
+  choose_qmajor(a.G, p->head_dim, &hpw, &wh, &wq);
+  a.wh = wh;
+  a.wq = wq;
+  a.n_qtiles = (a.L + 32 * wq - 1) / (32 * wq);
+  const hipError_t e = fa::launch_fwd(a, p->dtype, p->head_dim, hpw, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+}
+
+size_t fa_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seqlen,
+                              int32_t head_dim, int32_t window, int32_t sink) {
+  if (check_common(batch, heads_q, heads_kv, seqlen, head_dim, window, sink, 1.f, FA_DTYPE_BF16) != FA_OK)
+    return 0;
+  const SinkPlan sp = sink_plan(seqlen, window, sink);
+  return delta_bytes(batch, heads_q, seqlen) + partial_bytes(batch, heads_kv, head_dim, sp);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Validates a backward call and fills the kernel arguments; returns FA_OK or an fa_status.
+int prepare_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, fa::Args* out, int* hpw) {
+  const int rc = fa_check_bwd(p);
+  if (rc != FA_OK) return rc;
+  const size_t need = fa_bwd_workspace_bytes(p->batch, p->heads_q, p->heads_kv, p->seqlen, p->head_dim,
+                                             p->window, p->sink);
+  if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return FA_ERR_WORKSPACE;
+  fa::Args a = base_args(p->batch, p->heads_q, p->heads_kv, p->seqlen, p->head_dim, p->window, p->sink,
+                         p->softmax_scale);
+  a.q = p->q;
+  a.k = p->k;
+  a.v = p->v;
+  a.o = p->o;
+  a.dout = p->dout;
+  a.lse = p->lse;
+  a.dq = p->dq;
+  a.dk = p->dk;
+  a.dv = p->dv;
+  copy3(a.sq, p->q_stride);
+  copy3(a.sk, p->k_stride);
+  copy3(a.sv, p->v_stride);
+  copy3(a.so, p->o_stride);
+  copy3(a.sdo, p->do_stride);
+  copy3(a.slse, p->lse_stride);
+  copy3(a.sdq, p->dq_stride);
+  copy3(a.sdk, p->dk_stride);
+  copy3(a.sdv, p->dv_stride);
+  a.delta = static_cast<float*>(workspace);
+  a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + delta_bytes(a.B, a.Hq, a.L));
+
+  int wh, wq;
+  choose_qmajor(a.G, p->head_dim, hpw, &wh, &wq);
+  a.wh = wh;
+  a.wq = wq;
+  a.n_qtiles = (a.L + 32 * wq - 1) / (32 * wq);
+
+  const SinkPlan sp = sink_plan(a.L, p->window, p->sink);
+  a.n_kblocks = (a.L + 31) / 32;
+  a.nsp = sp.nsp;
+  a.n_chunks = sp.n_chunks;
+  a.chunk_rows = kChunkRows;
+  a.n_chunk_wgs = a.B * a.Hkv * a.nsp * a.n_chunks;
+  *out = a;
+  return FA_OK;
+}
+
+int run_dq(const fa::Args& a, const fa_bwd_params* p, int hpw, hipStream_t s) {
+  return fa::launch_bwd_dq(a, p->dtype, p->head_dim, hpw, s) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+}
+
+int run_dkdv(const fa::Args& a, const fa_bwd_params* p, hipStream_t s) {
+  if (fa::launch_bwd_dkdv(a, p->dtype, p->head_dim, s) != hipSuccess) return FA_ERR_LAUNCH;
+  if (a.nsp > 0 && fa::launch_bwd_sink_finalize(a, p->dtype, p->head_dim, s) != hipSuccess) return FA_ERR_LAUNCH;
+  return FA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {
+  fa::Args a;
+  int hpw = 1;
+  const int rc = prepare_bwd(p, workspace, workspace_bytes, &a, &hpw);
+  if (rc != FA_OK) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int r1 = run_dq(a, p, hpw, s);
+  return r1 != FA_OK ? r1 : run_dkdv(a, p, s);
+}
+
+int fa_bwd_dq(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {
+  fa::Args a;
+  int hpw = 1;
+  const int rc = prepare_bwd(p, workspace, workspace_bytes, &a, &hpw);
+  return rc != FA_OK ? rc : run_dq(a, p, hpw, static_cast<hipStream_t>(stream));
+}
+
+int fa_bwd_dkdv(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {
+  fa::Args a;
+  int hpw = 1;
+  const int rc = prepare_bwd(p, workspace, workspace_bytes, &a, &hpw);
+  return rc != FA_OK ? rc : run_dkdv(a, p, static_cast<hipStream_t>(stream));
+}
+
+const char* fa_strerror(int status) {
+  switch (status) {
+    case FA_OK: return "ok";
+    case FA_ERR_NULL: return "a required pointer is NULL";
+    case FA_ERR_SHAPE: return "invalid shape: batch, heads and seqlen must be >= 1 and heads_q % heads_kv == 0";
+    case FA_ERR_HEAD_DIM: return "head_dim must be one of 16, 32, 64, 128";
+    case FA_ERR_DTYPE: return "dtype must be FA_DTYPE_BF16 or FA_DTYPE_F16";
+    case FA_ERR_ALIGN: return "tensors must be 16-byte aligned with non-negative strides that are multiples of 8 elements (lse: 4-byte aligned, non-negative strides)";
+    case FA_ERR_MASK: return "window < 1 and sink < 1 leave every query row fully masked";
+    case FA_ERR_WORKSPACE: return "workspace is NULL, not 256-byte aligned or smaller than fa_bwd_workspace_bytes()";
+    case FA_ERR_LAUNCH: return "HIP kernel launch failed";
+    case FA_ERR_OVERFLOW: return "problem size exceeds the kernels' index range";
+    case FA_ERR_SCALE: return "softmax_scale must be finite";
+  }
+  return "unknown fa_status";
+}
+
+int fa_version(void) { return FA_GFX950_VERSION; }
+
+}  // extern "C"

@@ -1,0 +1,144 @@
+// fa_common.h - device building blocks shared by the gfx950 attention kernels.
+//
+// Every kernel in this library is written around one CDNA4 matrix instruction,
+// v_mfma_f32_32x32x16_{bf16,f16}: a wave64 multiplies a 32x16 A tile by a 16x32 B tile and
+// accumulates a 32x32 fp32 C tile.  Lane l (r = l % 32, h = l / 32) supplies
+//     A[r][8h .. 8h+7]   and   B[8h .. 8h+7][r]          (8 x 16-bit each)
+// and holds
+//     C[8*(i/4) + 4h + (i%4)][r]   for i = 0..15          (16 x fp32).
+// (Checked on hardware by an in-bounds probe before these kernels were written.)
+//
+// Two consequences shape the kernels:
+//  * The order of the 16 reduction indices inside one instruction is free as long as A and B
+//    agree, so each kernel picks whatever index order makes its loads contiguous.
+//  * A C tile holds, per lane, one column and 16 rows.  Feeding it back as the B operand of
+//    the next product (after a cast to 16 bit) needs no data movement if the next product's
+//    reduction index order is "rows 8j+4h..8j+4h+3 for j = 2t, 2t+1" in step t.  The matching
+//    A operand is staged in LDS with the middle two quads of every 16 swapped (perm16 below),
+//    so a lane reads its 8 A values with one 16-byte ds_read.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fa_plan.h"
+
+namespace fa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+// 16-bit element types.  `Elem` selects the MFMA flavour and the fp32 -> 16-bit cast
+// (round-to-nearest-even through v_cvt_pk_{bf16,f16}_f32).
+struct BF16 {
+  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    f32x2 v = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t bits) {
+    return __builtin_bit_cast(float, uint32_t(bits) << 16);
+  }
+};
+
+struct F16 {
+  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    f32x2 v = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t bits) {
+    return float(__builtin_bit_cast(_Float16, bits));
+  }
+};
+
+// Eight fp32 C values -> one 16-byte B operand.
+template <typename E>
+__device__ __forceinline__ u32x4 pack8(const float* x) {
+  u32x4 r;
+  r[0] = E::pack2(x[0], x[1]);
+  r[1] = E::pack2(x[2], x[3]);
+  r[2] = E::pack2(x[4], x[5]);
+  r[3] = E::pack2(x[6], x[7]);
+  return r;
+}
+
+// Dot product of two 16-byte vectors of 16-bit values, accumulated in fp32.
+template <typename E>
+__device__ __forceinline__ float dot8(u32x4 a, u32x4 b) {
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    s += E::to_f32(uint16_t(a[w])) * E::to_f32(uint16_t(b[w]));
+    s += E::to_f32(uint16_t(a[w] >> 16)) * E::to_f32(uint16_t(b[w] >> 16));
+  }
+  return s;
+}
+
+// Storage position of index r (0..15) inside a 16-group of a "permuted" LDS row: the middle
+// two quads are swapped, so lane half h finds C rows {4h..4h+3, 8+4h..8+4h+3} at positions
+// 8h..8h+7.
+__device__ __forceinline__ int perm16(int r) { return (r & 3) | ((r & 4) << 1) | ((r & 8) >> 1); }
+__device__ __forceinline__ int perm_pos(int idx) { return (idx & ~15) | perm16(idx & 15); }
+
+// Output-row order of the A operand for products whose C rows are the head dim: A row m holds
+// head-dim index sigma(m), so lane half h of a C tile owns head-dim indices 16h..16h+15 in
+// register order i = 0..15 (contiguous, storable with two 16-byte writes).
+__device__ __forceinline__ int sigma32(int m) { return ((m >> 2) & 1) * 16 + (m >> 3) * 4 + (m & 3); }
+
+// Global loads/stores of 16 bytes.
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ u32x4 zero16() { return u32x4{0u, 0u, 0u, 0u}; }
+
+// Exchange with the lane 32 positions away (the other half of the wave).
+__device__ __forceinline__ float xor32(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                       int((threadIdx.x ^ 32) & 63) << 2, __builtin_bit_cast(int, x)));
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// Map a linear workgroup id to a logical tile id so that every XCD (workgroups are dispatched
+// round-robin over the 8 XCDs) receives one contiguous range of logical tiles; neighbouring
+// tiles share K/V rows, which then stay in that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int id, int n) {
+  constexpr int kXcd = 8;
+  const int per = n / kXcd, rem = n % kXcd;
+  const int xcd = id % kXcd, pos = id / kXcd;
+  return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + pos;
+}
+
+// Four 16-byte rows of 8 x 16-bit values -> eight 8-byte columns (4 x 16-bit), i.e. the
+// 4x8 -> 8x4 transpose used to stage a [rows][d] tile as [d][rows] in LDS.
+__device__ __forceinline__ void transpose4x8(const u32x4 in[4], u32x2 out[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t a = in[0][w], b = in[1][w], c = in[2][w], d = in[3][w];
+    // column 2w takes the low halves, column 2w+1 the high halves
+    out[2 * w][0] = (a & 0xffffu) | (b << 16);
+    out[2 * w][1] = (c & 0xffffu) | (d << 16);
+    out[2 * w + 1][0] = (a >> 16) | (b & 0xffff0000u);
+    out[2 * w + 1][1] = (c >> 16) | (d & 0xffff0000u);
+  }
+}
+
+}  // namespace fa

@@ -1,0 +1,259 @@
+// fa_fwd.hip - forward pass: O = softmax(mask(Q K^T * scale)) V and the row log-sum-exp.
+//
+// Replaces _flash_attention_forward_swa_kernel (flash_attention_gpt_oss.py:7-180) and the
+// benchmark's _forward_kernel (benchmark_backward_speed.py:146-217).  Same mathematics (FA-2
+// online softmax in the log2 domain), a different decomposition:
+//
+//  * A workgroup is 4 waves covering 32*wq query rows of HPW*wh query heads of ONE KV group,
+//    so every K/V tile staged in LDS serves all of those heads.
+//  * Each wave owns 32 query rows x HPW heads and computes the transposed score tile
+//    S^T = K Q^T (keys x queries) on v_mfma_f32_32x32x16: the lane that holds column q of S^T
+//    owns query row q, so the row max / row sum / rescale of the online softmax are per-lane
+//    scalars and only one cross-half exchange is needed per 32-key step.
+//  * O^T = V^T P^T accumulates in registers; P^T goes from the C layout of S^T straight into
+//    the B operand (see fa_common.h), V^T is staged in LDS in the matching permuted order.
+//  * Key blocks are enumerated as in the reference: the sink blocks [0, min(S, ws)) and then the
+//    window blocks [ws, q_end) (ws = window start rounded down to the 64-key LDS block), and
+//    each wave additionally skips 32-key halves outside its own rows' window.  Tiles that are
+//    fully inside the mask skip the per-element mask.
+#include "fa_args.h"
+#include "fa_common.h"
+
+namespace fa {
+
+template <typename E, int D, int HPW>
+__global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
+  constexpr int BN = 64;                   // keys per LDS block
+  constexpr int KS = D / 16;               // reduction steps over the head dim
+  constexpr int DB = D >= 32 ? D / 32 : 1; // 32-row C tiles of O^T
+  constexpr int KROW = D + 8;              // K row stride in LDS (elements)
+  constexpr int VROW = BN + 8;             // V^T row stride in LDS (elements)
+  constexpr int BUF = BN * KROW + D * VROW;
+  constexpr int NK = (BN * D / 8 + 255) / 256;  // 16-byte K chunks per thread
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int r32 = lane & 31, hf = lane >> 5;
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = tile % a.n_qtiles;
+  const int hg = tile / a.n_qtiles;
+  const int hwg = HPW * a.wh;
+  const int groups_per_batch = a.Hq / hwg;
+  const int b = hg / groups_per_batch;
+  const int h0 = (hg % groups_per_batch) * hwg;
+  const int kvh = h0 / a.G;
+  const int BM = 32 * a.wq;
+  const int q0 = qt * BM;
+  const int qw = q0 + 32 * (wave % a.wq);
+  const int hw = h0 + HPW * (wave / a.wq);
+  const int q = qw + r32;
+  const bool wave_active = qw < a.L;
+  const int L = a.L, W = a.W, S = a.S;
+
+  // Q^T operand fragments: lane (q, hf) holds head-dim slice [hf*D/2 + 8ks, +8) in step ks.
+  u32x4 qf[HPW][KS];
+#pragma unroll
+  for (int h = 0; h < HPW; ++h) {
+    const char* qp = reinterpret_cast<const char*>(a.q) +
+                     2 * (int64_t(b) * a.sq[0] + int64_t(hw + h) * a.sq[1] + int64_t(q) * a.sq[2]);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 v = zero16();
+      if (q < L) v = ld16(qp + 2 * (hf * (D / 2) + 8 * ks));
+      v ^= a.qsign;
+      qf[h][ks] = v;
+    }
+  }
+
+  float m2[HPW], lsum[HPW];
+  f32x16 acc[HPW][DB];
+#pragma unroll
+  for (int h = 0; h < HPW; ++h) {
+    m2[h] = kNegInf;
+    lsum[h] = 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[h][db] = f32x16{};
+  }
+
+  // Key block enumeration for the workgroup's rows [q0, q_end).
+  const QPlan plan = qplan(q0, BM, L, W, S);
+
+  const char* kbase = reinterpret_cast<const char*>(a.k) + 2 * (int64_t(b) * a.sk[0] + int64_t(kvh) * a.sk[1]);
+  const char* vbase = reinterpret_cast<const char*>(a.v) + 2 * (int64_t(b) * a.sv[0] + int64_t(kvh) * a.sv[1]);
+
+  // Register staging of the next LDS block.
+  u32x4 kreg[NK];
+  u32x4 vreg[4];
+  const int v_dc = tid % (D / 8), v_kq = tid / (D / 8);  // V unit: 8 head-dim x 4 keys
+  const bool v_loader = tid < 2 * D;
+
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int it = 0; it < NK; ++it) {
+      const int c = tid + 256 * it;
+      const int row = c / (D / 8), col = c % (D / 8);
+      u32x4 v = zero16();
+      if (c < BN * D / 8 && kb + row < L) v = ld16(kbase + 2 * (int64_t(kb + row) * a.sk[2] + 8 * col));
+      kreg[it] = v;
+    }
+    if (v_loader) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb + 4 * v_kq + r;
+        u32x4 v = zero16();
+        if (key < L) v = ld16(vbase + 2 * (int64_t(key) * a.sv[2] + 8 * v_dc));
+        vreg[r] = v;
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+    uint16_t* Kl = lds + buf * BUF;
+    uint16_t* Vl = Kl + BN * KROW;
+#pragma unroll
+    for (int it = 0; it < NK; ++it) {
+      const int c = tid + 256 * it;
+      const int row = c / (D / 8), col = c % (D / 8);
+      if (c < BN * D / 8) st16(Kl + row * KROW + 8 * col, kreg[it]);
+    }
+    if (v_loader) {
+      u32x2 cols[8];
+      transpose4x8(vreg, cols);
+      const int pos = perm_pos(4 * v_kq);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        *reinterpret_cast<u32x2*>(Vl + (8 * v_dc + i) * VROW + pos) = cols[i];
+    }
+  };
+
+  gload(qplan_block(plan, 0));
+  sstore(0);
+  __syncthreads();
+
+  for (int i = 0; i < plan.nb; ++i) {
+    const int kb = qplan_block(plan, i);
+    const bool more = i + 1 < plan.nb;
+    if (more) gload(qplan_block(plan, i + 1));
+    if (wave_active) {
+      const uint16_t* Kl = lds + (i & 1) * BUF;
+      const uint16_t* Vl = Kl + BN * KROW;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        const int ks0 = kb + 32 * sb;
+        if (!wave_needs(ks0, qw, L, W, S)) continue;
+        // S^T = K Q^T for every head of the wave (the K fragment is shared).
+        f32x16 s[HPW];
+#pragma unroll
+        for (int h = 0; h < HPW; ++h) s[h] = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const u32x4 kf = *reinterpret_cast<const u32x4*>(Kl + (32 * sb + r32) * KROW + hf * (D / 2) + 8 * ks);
+#pragma unroll
+          for (int h = 0; h < HPW; ++h) s[h] = E::mfma(kf, qf[h][ks], s[h]);
+        }
+        const bool full = tile_full(ks0, qw, W, S);
+        u32x4 pb[HPW][2];
+#pragma unroll
+        for (int h = 0; h < HPW; ++h) {
+          float sv[16];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sv[e] = s[h][e];
+          if (!full) {
+            const int kl = ks0 + 4 * hf;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int off = 8 * (e / 4) + (e % 4);
+              if (!allowed(q - kl - off, kl + off, W, S)) sv[e] = kNegInf;
+            }
+          }
+          float mx = sv[0];
+#pragma unroll
+          for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sv[e]);
+          mx = fmaxf(mx, xor32(mx));
+          const float mxs = mx == kNegInf ? kNegInf : mx * a.c;
+          const float mnew = fmaxf(m2[h], mxs);
+          const float alpha = mnew == kNegInf ? 1.f : fast_exp2(m2[h] - mnew);
+          const float ms = mnew == kNegInf ? 0.f : mnew;
+          float ps = 0.f;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            sv[e] = fast_exp2(fmaf(sv[e], a.c, -ms));
+            ps += sv[e];
+          }
+          lsum[h] = lsum[h] * alpha + ps;
+          m2[h] = mnew;
+#pragma unroll
+          for (int db = 0; db < DB; ++db) acc[h][db] *= alpha;
+          pb[h][0] = pack8<E>(sv);
+          pb[h][1] = pack8<E>(sv + 8);
+        }
+        // O^T += V^T P^T (the V^T fragment is shared by the heads).
+        const int vrow = sigma32(r32);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            u32x4 vf = zero16();
+            if (D >= 32 || vrow < D)
+              vf = *reinterpret_cast<const u32x4*>(Vl + (32 * db + vrow) * VROW + 32 * sb + 16 * t + 8 * hf);
+#pragma unroll
+            for (int h = 0; h < HPW; ++h) acc[h][db] = E::mfma(vf, pb[h][t], acc[h][db]);
+          }
+        }
+      }
+    }
+    if (more) sstore((i + 1) & 1);
+    __syncthreads();
+  }
+
+  if (!wave_active) return;
+#pragma unroll
+  for (int h = 0; h < HPW; ++h) {
+    const float lt = lsum[h] + xor32(lsum[h]);
+    if (q >= L) continue;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    char* op = reinterpret_cast<char*>(a.o_out) +
+               2 * (int64_t(b) * a.so_out[0] + int64_t(hw + h) * a.so_out[1] + int64_t(q) * a.so_out[2]);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      if (D == 16 && hf == 1) continue;
+      float ov[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ov[e] = acc[h][db][e] * inv;
+      const int d0 = 32 * db + (D >= 32 ? 16 * hf : 0);
+      st16(op + 2 * d0, pack8<E>(ov));
+      st16(op + 2 * (d0 + 8), pack8<E>(ov + 8));
+    }
+    if (hf == 0) {
+      a.lse_out[int64_t(b) * a.slse[0] + int64_t(hw + h) * a.slse[1] + int64_t(q) * a.slse[2]] =
+          (m2[h] + fast_log2(lt)) * kLn2;
+    }
+  }
+}
+
+template <typename E, int D>
+static hipError_t launch_fwd_d(const Args& a, int hpw, hipStream_t stream) {
+  const int groups = a.B * a.Hq / (hpw * a.wh);
+  const dim3 grid(a.n_qtiles * groups), block(256);
+  if (hpw == 2) hipLaunchKernelGGL((fwd_kernel<E, D, 2>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((fwd_kernel<E, D, 1>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+template <typename E>
+static hipError_t launch_fwd_e(const Args& a, int D, int hpw, hipStream_t stream) {
+  switch (D) {
+    case 16: return launch_fwd_d<E, 16>(a, hpw, stream);
+    case 32: return launch_fwd_d<E, 32>(a, hpw, stream);
+    case 64: return launch_fwd_d<E, 64>(a, hpw, stream);
+    case 128: return launch_fwd_d<E, 128>(a, hpw, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stream) {
+  return dtype == 1 ? launch_fwd_e<BF16>(a, D, hpw, stream) : launch_fwd_e<F16>(a, D, hpw, stream);
+}
+
+}  // namespace fa

@@ -1,0 +1,87 @@
+// fa_plan.h - which key blocks / query rows each workgroup and wave visits.
+//
+// Shared by the kernels (device) and by the host: fa_capi.cpp sizes the sink split with it, and
+// tests/plan_check.cpp compiles this same header with g++ (FA_HOST_ONLY) to check that every
+// allowed (query, key) pair is visited exactly once.  W and S are the clamped window and sink
+// (0 <= W, S <= L).
+//
+// Mask (benchmark_backward_speed.py:40-46): allowed(q, k) = k <= q && (q - k < W || k < S).
+#pragma once
+
+#ifdef FA_HOST_ONLY
+#define FA_HD inline
+#else
+#include <hip/hip_runtime.h>
+#define FA_HD __host__ __device__ __forceinline__
+#endif
+
+namespace fa {
+
+constexpr int kLdsKeys = 64;  // keys per LDS block of the query-major kernels
+constexpr int kStep = 32;     // keys (or query rows) per MFMA tile edge
+
+FA_HD int imin(int a, int b) { return a < b ? a : b; }
+FA_HD int imax(int a, int b) { return a > b ? a : b; }
+
+// dq = q - k
+FA_HD bool allowed(int dq, int k, int W, int S) { return dq >= 0 && (dq < W || k < S); }
+
+// ---- query-major kernels (forward, dQ) --------------------------------------------------------
+// A workgroup owns rows [q0, q0 + bm).  It visits, in LDS blocks of 64 keys, the sink blocks
+// [0, min(S, ws)) and then the window blocks [ws, min(q0 + bm, L)), where ws is the first key
+// any of its rows can see through the window, rounded down to 64 (the two-phase order of
+// benchmark_backward_speed.py:185-208; flash_attention_gpt_oss.py:59-167 has the same idea with
+// a separate diagonal phase).  Sink blocks end at or before ws, so no key is visited twice.
+struct QPlan {
+  int ws, nsb, nb;
+};
+
+FA_HD QPlan qplan(int q0, int bm, int L, int W, int S) {
+  QPlan p;
+  const int q_end = imin(q0 + bm, L);
+  p.ws = (imax(0, q0 - W + 1) / kLdsKeys) * kLdsKeys;
+  const int sink_end = imin(S, p.ws);
+  p.nsb = (sink_end + kLdsKeys - 1) / kLdsKeys;
+  p.nb = p.nsb + (q_end - p.ws + kLdsKeys - 1) / kLdsKeys;
+  return p;
+}
+
+FA_HD int qplan_block(const QPlan& p, int i) { return i < p.nsb ? i * kLdsKeys : p.ws + (i - p.nsb) * kLdsKeys; }
+
+// Does the wave owning rows [qw, qw + 32) need the 32 keys starting at ks0?  (Sinks, or an
+// overlap with its own window [qw - W + 1, qw + 31].)
+FA_HD bool wave_needs(int ks0, int qw, int L, int W, int S) {
+  const int lo = qw - W + 1, hi = imin(qw + 31, L - 1);
+  return ks0 < S || (ks0 + 31 >= lo && ks0 <= hi);
+}
+
+// Is every pair of rows [qr, qr + 32) x keys [ks0, ks0 + 32) allowed?  (Then the kernels skip
+// the per-element mask.  Rows >= L may be included: their results are never stored.)
+FA_HD bool tile_full(int ks0, int qr, int W, int S) {
+  return (ks0 + 31 <= qr) && ((qr + 31 - ks0 < W) || (ks0 + 32 <= S));
+}
+
+// ---- key-major kernel (dK, dV) ----------------------------------------------------------------
+// Key block kblk = keys [32 kblk, 32 kblk + 32).  Its regular workgroup covers rows
+// [32 kblk, kv_window_end): every window pair of the block lies there.  For the first `nsp`
+// blocks (those holding sink keys with rows beyond kv_window_end) the remaining rows
+// [kv_window_end, L) only see the sink keys; they are split into chunks of chunk_rows handled by
+// extra workgroups, chunk c covering [max(c*chunk_rows, end), min((c+1)*chunk_rows, L)).
+FA_HD int kv_window_end(int kblk, int L, int W) { return imin(L, kStep * kblk + kStep - 1 + W); }
+
+FA_HD int kv_chunk_lo(int kblk, int c, int chunk_rows, int L, int W) {
+  return imax(c * chunk_rows, kv_window_end(kblk, L, W));
+}
+
+FA_HD int kv_chunk_hi(int c, int chunk_rows, int L) { return imin((c + 1) * chunk_rows, L); }
+
+// Number of leading key blocks whose sink rows are chunked: blocks holding a key < S whose
+// window end is before L.  (Both conditions hold on a prefix of the blocks.)
+FA_HD int kv_sink_blocks(int L, int W, int S) {
+  int n = 0;
+  for (int kb = 0; kStep * kb < S; ++kb)
+    if (kv_window_end(kb, L, W) < L) n = kb + 1;
+  return n;
+}
+
+}  // namespace fa

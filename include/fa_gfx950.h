@@ -1,0 +1,150 @@
+/*
+ * fa_gfx950.h - C ABI of the MI355X (gfx950) sliding-window + sink FlashAttention-2 library.
+ *
+ * The library computes causal attention with grouped-query heads (Hq query heads share Hkv
+ * key/value heads, head h reads KV head h / (Hq/Hkv)), a sliding window W and S positional
+ * "sink" keys:
+ *
+ *     allowed(q, k) = k <= q  &&  (q - k < W  ||  k < S)
+ *
+ * (reference predicate: benchmark_backward_speed.py:40-46 create_mask_bool and :110-115
+ * _compute_mask; flash_attention_gpt_oss.py:82-86, 116-120, 150-155 for the repo kernels).
+ *
+ * Layouts follow the reference autograd function (flash_attention_gpt_oss.py:340-438):
+ * q/o/dout/dq are [B, Hq, L, D], k/v/dk/dv are [B, Hkv, L, D], lse is float32 [B, Hq, L].
+ * Every tensor is described by a base pointer and its batch/head/sequence strides in elements;
+ * the head-dim stride must be 1.  lse holds the natural-log log-sum-exp of the scaled, masked
+ * scores of each query row (the reference repo keeps a log2-domain row max instead,
+ * flash_attention_gpt_oss.py:178-180; the statistic never leaves the autograd context).
+ *
+ * Rules shared by every entry point:
+ *   - the library never allocates or frees device memory; the caller passes every buffer,
+ *     including the backward workspace sized by fa_bwd_workspace_bytes();
+ *   - launches are asynchronous on `stream` (a hipStream_t; NULL means the legacy default
+ *     stream); nothing synchronises the host;
+ *   - arguments are validated on the host before any HIP call; on failure a negative FA_ERR_*
+ *     code is returned and nothing is launched.  fa_strerror() names each code;
+ *   - the library holds no mutable global state, so concurrent calls on different streams are
+ *     safe.
+ */
+#ifndef FA_GFX950_H
+#define FA_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_GFX950_VERSION 10000 /* 1.0.0 */
+
+/* Element types of q/k/v/o/dout/dq/dk/dv.  All of them share one type per call. */
+enum fa_dtype { FA_DTYPE_BF16 = 1, FA_DTYPE_F16 = 2 };
+
+enum fa_status {
+  FA_OK = 0,
+  FA_ERR_NULL = -1,        /* a required pointer is NULL */
+  FA_ERR_SHAPE = -2,       /* B, Hq, Hkv or L < 1, or Hq % Hkv != 0 */
+  FA_ERR_HEAD_DIM = -3,    /* D not in {16, 32, 64, 128} */
+  FA_ERR_DTYPE = -4,       /* dtype not an fa_dtype */
+  FA_ERR_ALIGN = -5,       /* a 16-bit tensor's base not 16-byte aligned, or a stride negative or
+                              not a multiple of 8 elements; lse not 4-byte aligned */
+  FA_ERR_MASK = -6,        /* window < 1 and sink < 1: every query row would be fully masked */
+  FA_ERR_WORKSPACE = -7,   /* workspace NULL or smaller than fa_bwd_workspace_bytes() */
+  FA_ERR_LAUNCH = -8,      /* a HIP launch failed */
+  FA_ERR_OVERFLOW = -9,    /* a size or element offset does not fit the kernels' index math */
+  FA_ERR_SCALE = -10       /* softmax_scale is NaN or infinite */
+};
+
+/* Forward pass.  Replaces the launch in FlashSWDAWithSink.forward
+ * (flash_attention_gpt_oss.py:341-385) and the Triton _forward_kernel of the benchmark
+ * (benchmark_backward_speed.py:146-217). */
+typedef struct fa_fwd_params {
+  const void* q;          /* [B, Hq, L, D]  */
+  const void* k;          /* [B, Hkv, L, D] */
+  const void* v;          /* [B, Hkv, L, D] */
+  void* o;                /* [B, Hq, L, D]  output */
+  float* lse;             /* [B, Hq, L]     output, natural-log log-sum-exp */
+  int64_t q_stride[3];    /* batch, head, sequence strides in elements */
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+  int64_t o_stride[3];
+  int64_t lse_stride[3];  /* any non-negative strides; lse needs 4-byte alignment only */
+  int32_t batch, heads_q, heads_kv, seqlen, head_dim;
+  int32_t window;         /* W: key k is in the window of query q when q - k < W */
+  int32_t sink;           /* S: keys k < S are visible to every query q >= k */
+  float softmax_scale;    /* the reference default is 1/sqrt(D), flash_attention_gpt_oss.py:345-346 */
+  int32_t dtype;          /* enum fa_dtype */
+} fa_fwd_params;
+
+/* Backward pass.  Replaces FlashSWDAWithSink.backward's delta computation and kernel launch
+ * (flash_attention_gpt_oss.py:387-435) and the split dQ / dK-dV kernels of the benchmark
+ * (benchmark_backward_speed.py:312-466, 574-612).  dq, dk and dv are written in the input
+ * dtype; dk and dv are complete sums over the Hq/Hkv query heads of each group, computed
+ * without atomics, so reruns are bitwise identical. */
+typedef struct fa_bwd_params {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;          /* forward output */
+  const void* dout;       /* gradient of the loss with respect to o */
+  const float* lse;       /* forward statistic from fa_fwd */
+  void* dq;               /* [B, Hq, L, D]  output */
+  void* dk;               /* [B, Hkv, L, D] output */
+  void* dv;               /* [B, Hkv, L, D] output */
+  int64_t q_stride[3];
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+  int64_t o_stride[3];
+  int64_t do_stride[3];
+  int64_t lse_stride[3];
+  int64_t dq_stride[3];
+  int64_t dk_stride[3];
+  int64_t dv_stride[3];
+  int32_t batch, heads_q, heads_kv, seqlen, head_dim;
+  int32_t window;
+  int32_t sink;
+  float softmax_scale;
+  int32_t dtype;
+} fa_bwd_params;
+
+/* Launches the forward kernel.  Returns FA_OK or a negative fa_status. */
+int fa_fwd(const fa_fwd_params* p, void* stream);
+
+/* Bytes of device workspace fa_bwd needs for this problem (row statistics of the backward and
+ * per-chunk partial sums for the sink keys).  Returns 0 for an invalid problem.  The
+ * reference instead allocates fp32 dK/dV staging buffers inside backward
+ * (flash_attention_gpt_oss.py:397-400). */
+size_t fa_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seqlen,
+                              int32_t head_dim, int32_t window, int32_t sink);
+
+/* Launches the backward kernels (fa_bwd_dq then fa_bwd_dkdv).  `workspace` must hold
+ * fa_bwd_workspace_bytes() bytes of device memory, 256-byte aligned; its contents on entry do
+ * not matter. */
+int fa_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The two stages of fa_bwd, for callers that schedule or time them separately.
+ * fa_bwd_dq computes dq and stores the row statistic delta = rowsum(dout * o) in the workspace
+ * (replaces the _backward_dq_kernel launch, benchmark_backward_speed.py:586-596, and the delta
+ * computation of flash_attention_gpt_oss.py:403).  fa_bwd_dkdv computes dk and dv from that
+ * workspace (replaces the _backward_dkdv_kernel launch, benchmark_backward_speed.py:600-611); it
+ * must run after fa_bwd_dq on the same workspace, in stream order. */
+int fa_bwd_dq(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
+int fa_bwd_dkdv(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Host-only argument checks used by fa_fwd / fa_bwd (no HIP call is made). */
+int fa_check_fwd(const fa_fwd_params* p);
+int fa_check_bwd(const fa_bwd_params* p);
+
+/* Static text for a status code. */
+const char* fa_strerror(int status);
+
+/* FA_GFX950_VERSION of the built library. */
+int fa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_GFX950_H */

@@ -1,0 +1,117 @@
+"""TEST INFRASTRUCTURE ONLY: restatement of the reference's naive attention.
+
+Follows benchmark_backward_speed.py:40-54 (mask, KV repeat) and :68-85
+(pytorch_naive_attention).  See oracle/__init__.py for how each function is pinned.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+
+def allowed_mask(seq_len: int, window_size: int, sink_size: int, device=None) -> torch.Tensor:
+    """[L, L] bool, True where query row q may attend key column k:
+    k <= q and (q - k < W or k < S).  Same predicate as create_mask_bool
+    (benchmark_backward_speed.py:40-46): its sliding term col >= row - (W-1) is q - k < W."""
+    pos = torch.arange(seq_len, device=device)
+    qq = pos.view(-1, 1)
+    kk = pos.view(1, -1)
+    return (kk <= qq) & (((qq - kk) < window_size) | (kk < sink_size))
+
+
+def expand_kv(x: torch.Tensor, group: int) -> torch.Tensor:
+    """[B, Hkv, L, D] -> [B, Hkv*group, L, D], head h reading KV head h // group
+    (repeat_kv, benchmark_backward_speed.py:49-54)."""
+    return x if group == 1 else x.repeat_interleave(group, dim=1)
+
+
+def naive_attention(q, k, v, window_size: int, sink_size: int, scale: Optional[float] = None):
+    """The reference's baseline path, in the input dtype: dense scores in q's dtype, boolean
+    mask, softmax accumulated in float32 then cast back, probabilities @ V
+    (benchmark_backward_speed.py:68-85).  Autograd provides its backward."""
+    group = q.shape[1] // k.shape[1]
+    k = expand_kv(k, group)
+    v = expand_kv(v, group)
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    scores = torch.matmul(q, k.transpose(-1, -2).contiguous()) * scale
+    keep = allowed_mask(q.shape[2], window_size, sink_size, device=q.device)
+    scores = scores.masked_fill(~keep, float("-inf"))
+    probs = torch.softmax(scores, dim=-1, dtype=torch.float32).to(q.dtype)
+    return torch.matmul(probs, v)
+
+
+@torch.no_grad()
+def attention_fwd_bwd(q, k, v, do, window_size: int, sink_size: int, scale: Optional[float] = None,
+                      compute_dtype=torch.float32, row_chunk: Optional[int] = None, heads=None):
+    """Explicit forward and backward of masked attention, evaluated in `compute_dtype`.
+
+    Returns (o, lse, dq, dk, dv) in compute_dtype on the inputs' device, with
+      s = scale * q.k over allowed keys, lse = logsumexp(s) (natural log), P = exp(s - lse),
+      o = P V, delta = rowsum(dO o O), dS = P (dO V^T - delta),
+      dq = scale * dS K, dk = scale * sum_heads dS^T Q, dv = sum_heads P^T dO.
+    Work is done one (batch, query head) at a time and `row_chunk` query rows at a time, so
+    memory stays at row_chunk x L scores.  `heads` optionally restricts the query heads that
+    are evaluated (dq/o/lse of other heads stay 0; dk/dv then only sum the listed heads).
+    """
+    B, Hq, L, D = q.shape
+    Hkv = k.shape[1]
+    group = Hq // Hkv
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    R = L if row_chunk is None else int(row_chunk)
+    qf, kf, vf, gf = (t.to(compute_dtype) for t in (q, k, v, do))
+    o = torch.zeros_like(qf)
+    lse = torch.zeros((B, Hq, L), dtype=compute_dtype, device=q.device)
+    dq = torch.zeros_like(qf)
+    dk = torch.zeros_like(kf)
+    dv = torch.zeros_like(vf)
+    pos = torch.arange(L, device=q.device)
+    head_list = range(Hq) if heads is None else heads
+    for b in range(B):
+        for h in head_list:
+            g = h // group
+            K, V = kf[b, g], vf[b, g]
+            Kt, Vt = K.t().contiguous(), V.t().contiguous()
+            for r0 in range(0, L, R):
+                r1 = min(L, r0 + R)
+                rows = pos[r0:r1].view(-1, 1)
+                keep = (pos.view(1, -1) <= rows) & (((rows - pos.view(1, -1)) < window_size) |
+                                                    (pos.view(1, -1) < sink_size))
+                Q, G = qf[b, h, r0:r1], gf[b, h, r0:r1]
+                s = torch.matmul(Q, Kt) * scale
+                s = s.masked_fill(~keep, float("-inf"))
+                m = torch.logsumexp(s, dim=-1)
+                p = torch.exp(s - m.view(-1, 1))
+                ob = torch.matmul(p, V)
+                dp = torch.matmul(G, Vt)
+                delta = (G * ob).sum(dim=-1, keepdim=True)
+                ds = p * (dp - delta)
+                o[b, h, r0:r1] = ob
+                lse[b, h, r0:r1] = m
+                dq[b, h, r0:r1] = torch.matmul(ds, K) * scale
+                dk[b, g] += torch.matmul(ds.t().contiguous(), Q) * scale
+                dv[b, g] += torch.matmul(p.t().contiguous(), G)
+    return o, lse, dq, dk, dv
+
+
+class OracleAttention(torch.autograd.Function):
+    """attention_fwd_bwd behind autograd (float64 on CPU), so torch.autograd.gradcheck can
+    compare its explicit backward with finite differences of its forward."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, window_size, sink_size, scale):
+        ctx.save_for_backward(q, k, v)
+        ctx.cfg = (window_size, sink_size, scale)
+        o, _, _, _, _ = attention_fwd_bwd(q, k, v, torch.zeros_like(q), window_size, sink_size, scale,
+                                          compute_dtype=q.dtype)
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v = ctx.saved_tensors
+        window_size, sink_size, scale = ctx.cfg
+        _, _, dq, dk, dv = attention_fwd_bwd(q, k, v, do, window_size, sink_size, scale, compute_dtype=q.dtype)
+        return dq, dk, dv, None, None, None

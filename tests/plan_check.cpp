@@ -1,0 +1,125 @@
+// plan_check.cpp - host check of the kernels' visit plan (csrc/fa_plan.h compiled with g++).
+//
+// Walks the loops of the query-major kernels (fa_fwd.hip fwd_kernel, fa_bwd.hip bwd_dq_kernel)
+// and of the key-major kernel (bwd_dkdv_kernel) over many (L, W, S, rows-per-workgroup,
+// chunk size) cases and checks that
+//   * every allowed (q, k) pair is visited exactly once and no other pair is counted,
+//   * a tile reported "full" (mask skipped) holds only allowed pairs,
+//   * the key-major row ranges of the regular and chunk workgroups partition the rows that can
+//     see each key block.
+// Prints "OK <cases>" or the first failing case; exit status 0 on success.
+#define FA_HOST_ONLY 1
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+#include "../flashattention-gpt-oss-finetuning_amd/csrc/fa_plan.h"
+
+using namespace fa;
+
+static bool ref_allowed(int q, int k, int W, int S) { return k <= q && (q - k < W || k < S); }
+
+static int fail(const char* what, int L, int W, int S, int x, int q, int k, int got) {
+  std::printf("FAIL %s L=%d W=%d S=%d param=%d q=%d k=%d count=%d\n", what, L, W, S, x, q, k, got);
+  return 1;
+}
+
+// Query-major: workgroups of bm = 32*wq rows, waves of 32 rows.
+static int check_qmajor(int L, int W, int S, int wq) {
+  const int bm = 32 * wq;
+  std::vector<int> cnt(size_t(L) * L, 0);
+  for (int q0 = 0; q0 < L; q0 += bm) {
+    const QPlan p = qplan(q0, bm, L, W, S);
+    for (int i = 0; i < p.nb; ++i) {
+      const int kb = qplan_block(p, i);
+      if (kb < 0 || kb >= L) return fail("block out of range", L, W, S, wq, q0, kb, 0);
+      for (int w = 0; w < wq; ++w) {
+        const int qw = q0 + 32 * w;
+        if (qw >= L) continue;  // the kernel skips inactive waves
+        for (int sb = 0; sb < 2; ++sb) {
+          const int ks0 = kb + 32 * sb;
+          if (!wave_needs(ks0, qw, L, W, S)) continue;
+          const bool full = tile_full(ks0, qw, W, S);
+          for (int r = 0; r < 32; ++r)
+            for (int c = 0; c < 32; ++c) {
+              const int q = qw + r, k = ks0 + c;
+              if (q >= L) continue;  // rows >= L are never stored
+              const bool ok = full || allowed(q - k, k, W, S);
+              if (full && !(k < L && ref_allowed(q, k, W, S))) return fail("full tile has a masked pair", L, W, S, wq, q, k, 0);
+              if (ok && k < L) ++cnt[size_t(q) * L + k];
+              if (ok && k >= L) return fail("key beyond L passes the mask", L, W, S, wq, q, k, 0);
+            }
+        }
+      }
+    }
+  }
+  for (int q = 0; q < L; ++q)
+    for (int k = 0; k < L; ++k) {
+      const int want = ref_allowed(q, k, W, S) ? 1 : 0;
+      if (cnt[size_t(q) * L + k] != want) return fail("q-major visit count", L, W, S, wq, q, k, cnt[size_t(q) * L + k]);
+    }
+  return 0;
+}
+
+// Key-major: regular workgroups per 32-key block, plus chunk workgroups for the sink blocks.
+static int check_kvmajor(int L, int W, int S, int chunk_rows) {
+  std::vector<int> cnt(size_t(L) * L, 0);
+  const int nkb = (L + 31) / 32;
+  const int nsp = kv_sink_blocks(L, W, S);
+  const int n_chunks = nsp > 0 ? (L + chunk_rows - 1) / chunk_rows : 0;
+  auto sweep = [&](int kblk, int qlo, int qhi) -> int {
+    const int ks0 = 32 * kblk;
+    if (qhi <= qlo) return 0;
+    for (int qb = qlo / 32; qb < (qhi + 31) / 32; ++qb) {
+      const int qr0 = 32 * qb;
+      const bool full = (qr0 >= qlo) && (qr0 + 32 <= qhi) && tile_full(ks0, qr0, W, S);
+      for (int r = 0; r < 32; ++r)
+        for (int c = 0; c < 32; ++c) {
+          const int q = qr0 + r, k = ks0 + c;
+          const bool ok = full || (q >= qlo && q < qhi && allowed(q - k, k, W, S));
+          if (!ok) continue;
+          if (q >= L || k >= L) {
+            if (full) return fail("full kv tile beyond L", L, W, S, chunk_rows, q, k, 0);
+            return fail("kv pair beyond L passes", L, W, S, chunk_rows, q, k, 0);
+          }
+          if (full && !ref_allowed(q, k, W, S)) return fail("full kv tile has a masked pair", L, W, S, chunk_rows, q, k, 0);
+          ++cnt[size_t(q) * L + k];
+        }
+    }
+    return 0;
+  };
+  for (int kblk = 0; kblk < nkb; ++kblk)
+    if (sweep(kblk, 32 * kblk, kv_window_end(kblk, L, W))) return 1;
+  for (int kblk = 0; kblk < nsp; ++kblk)
+    for (int c = 0; c < n_chunks; ++c)
+      if (sweep(kblk, kv_chunk_lo(kblk, c, chunk_rows, L, W), kv_chunk_hi(c, chunk_rows, L))) return 1;
+  for (int q = 0; q < L; ++q)
+    for (int k = 0; k < L; ++k) {
+      const int want = ref_allowed(q, k, W, S) ? 1 : 0;
+      if (cnt[size_t(q) * L + k] != want) return fail("kv-major visit count", L, W, S, chunk_rows, q, k, cnt[size_t(q) * L + k]);
+    }
+  return 0;
+}
+
+int main() {
+  const int Ls[] = {1, 2, 5, 31, 32, 33, 63, 64, 65, 100, 127, 128, 129, 200, 257, 300, 513};
+  const int Ws[] = {0, 1, 2, 5, 31, 32, 33, 64, 100, 128, 129, 256, 100000};
+  const int Ss[] = {0, 1, 4, 16, 31, 32, 33, 64, 65, 100, 100000};
+  long cases = 0;
+  for (int L : Ls)
+    for (int Wr : Ws)
+      for (int Sr : Ss) {
+        if (Wr < 1 && Sr < 1) continue;  // rejected by the C ABI
+        const int W = Wr > L ? L : Wr, S = Sr > L ? L : Sr;  // clamped as in fa_capi.cpp
+        for (int wq : {1, 2, 4}) {
+          if (check_qmajor(L, W, S, wq)) return 1;
+          ++cases;
+        }
+        for (int cr : {32, 64, 256}) {
+          if (check_kvmajor(L, W, S, cr)) return 1;
+          ++cases;
+        }
+      }
+  std::printf("OK %ld\n", cases);
+  return 0;
+}

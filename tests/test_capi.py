@@ -1,0 +1,185 @@
+"""CPU tests of the C ABI: the library loads, exports what include/fa_gfx950.h declares, and its
+host-side validation returns the documented codes.  No kernel is launched (only argument
+errors are exercised, which return before any HIP call)."""
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from conftest import ROOT, load_mod
+
+_lib = load_mod("_lib")
+HEADER = os.path.join(ROOT, "include", "fa_gfx950.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\**\s*(fa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_python_export_list():
+    assert _declared_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in _declared_functions():
+        assert hasattr(L, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (fa_\w+)$", out, flags=re.M))
+    assert set(_declared_functions()) <= exported
+
+
+def test_version_and_strerror():
+    L = _lib.lib()
+    assert L.fa_version() == 10000
+    codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10]
+    texts = [_lib.strerror(c) for c in codes]
+    assert len(set(texts)) == len(codes)
+    assert _lib.strerror(12345) == "unknown fa_status"
+
+
+def test_struct_layouts_match_header():
+    # the ctypes mirrors must have the C layout: 5 pointers + 5 x 3 int64 + 7 int32 + float + int32
+    assert ctypes.sizeof(_lib.FwdParams) == 5 * 8 + 15 * 8 + 9 * 4 + 4  # padded to 8
+    assert ctypes.sizeof(_lib.BwdParams) == 9 * 8 + 27 * 8 + 9 * 4 + 4
+    # a C compiler agrees
+    src = (
+        '#include "fa_gfx950.h"\n#include <stdio.h>\n#include <stddef.h>\n'
+        "int main(void){printf(\"%zu %zu %zu %zu\\n\", sizeof(fa_fwd_params), sizeof(fa_bwd_params),"
+        " offsetof(fa_fwd_params, batch), offsetof(fa_bwd_params, softmax_scale));return 0;}\n"
+    )
+    tmp = tempfile.mkdtemp(prefix="fa_layout_")
+    cfile, exe = os.path.join(tmp, "layout.c"), os.path.join(tmp, "layout")
+    with open(cfile, "w") as f:
+        f.write(src)
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), cfile, "-o", exe], check=True)
+    vals = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
+    assert vals == [ctypes.sizeof(_lib.FwdParams), ctypes.sizeof(_lib.BwdParams),
+                    _lib.FwdParams.batch.offset, _lib.BwdParams.softmax_scale.offset]
+
+
+def _fwd_params(**over):
+    p = _lib.FwdParams()
+    B, Hq, Hkv, L, D = 1, 8, 2, 128, 64
+    fake = 1 << 20  # 16-byte aligned non-null addresses; never dereferenced (validation fails first or no launch)
+    p.q, p.k, p.v, p.o, p.lse = fake, fake, fake, fake, fake
+    p.q_stride[:] = (Hq * L * D, L * D, D)
+    p.k_stride[:] = (Hkv * L * D, L * D, D)
+    p.v_stride[:] = (Hkv * L * D, L * D, D)
+    p.o_stride[:] = (Hq * L * D, L * D, D)
+    p.lse_stride[:] = (Hq * L, L, 1)
+    p.batch, p.heads_q, p.heads_kv, p.seqlen, p.head_dim = B, Hq, Hkv, L, D
+    p.window, p.sink, p.softmax_scale, p.dtype = 16, 4, 0.125, _lib.FA_DTYPE_BF16
+    for k, v in over.items():
+        if k.endswith("_stride"):
+            getattr(p, k)[:] = v
+        else:
+            setattr(p, k, v)
+    return p
+
+
+def _bwd_params(**over):
+    p = _lib.BwdParams()
+    f = _fwd_params()
+    for name in ("q", "k", "v", "o", "lse"):
+        setattr(p, name, getattr(f, name))
+    p.dout, p.dq, p.dk, p.dv = f.q, f.q, f.k, f.v
+    for name in ("q", "k", "v", "o", "lse"):
+        getattr(p, name + "_stride")[:] = getattr(f, name + "_stride")[:]
+    p.do_stride[:] = f.q_stride[:]
+    p.dq_stride[:] = f.q_stride[:]
+    p.dk_stride[:] = f.k_stride[:]
+    p.dv_stride[:] = f.v_stride[:]
+    for name in ("batch", "heads_q", "heads_kv", "seqlen", "head_dim", "window", "sink", "softmax_scale", "dtype"):
+        setattr(p, name, getattr(f, name))
+    for k, v in over.items():
+        if k.endswith("_stride"):
+            getattr(p, k)[:] = v
+        else:
+            setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("over,code", [
+    ({}, _lib.FA_OK),
+    ({"q": None}, _lib.FA_ERR_NULL),
+    ({"lse": None}, _lib.FA_ERR_NULL),
+    ({"heads_q": 6}, _lib.FA_ERR_SHAPE),          # 6 % 4 != 0 ... with Hkv = 2 it divides; set below
+    ({"batch": 0}, _lib.FA_ERR_SHAPE),
+    ({"seqlen": 0}, _lib.FA_ERR_SHAPE),
+    ({"heads_kv": 3}, _lib.FA_ERR_SHAPE),
+    ({"head_dim": 48}, _lib.FA_ERR_HEAD_DIM),
+    ({"head_dim": 256}, _lib.FA_ERR_HEAD_DIM),
+    ({"head_dim": 8}, _lib.FA_ERR_HEAD_DIM),
+    ({"dtype": 0}, _lib.FA_ERR_DTYPE),
+    ({"dtype": 3}, _lib.FA_ERR_DTYPE),
+    ({"window": 0, "sink": 0}, _lib.FA_ERR_MASK),
+    ({"window": -5, "sink": 0}, _lib.FA_ERR_MASK),
+    ({"q": (1 << 20) + 8}, _lib.FA_ERR_ALIGN),
+    ({"lse": (1 << 20) + 2}, _lib.FA_ERR_ALIGN),
+    ({"q_stride": (8 * 128 * 64, 128 * 64, 68)}, _lib.FA_ERR_ALIGN),
+    ({"k_stride": (-8, 128 * 64, 64)}, _lib.FA_ERR_ALIGN),
+    ({"softmax_scale": float("nan")}, _lib.FA_ERR_SCALE),
+    ({"softmax_scale": float("inf")}, _lib.FA_ERR_SCALE),
+    ({"seqlen": (1 << 28) + 1}, _lib.FA_ERR_OVERFLOW),
+])
+def test_check_fwd_codes(over, code):
+    if over == {"heads_q": 6}:
+        over = {"heads_q": 6, "heads_kv": 4}
+    assert _lib.lib().fa_check_fwd(ctypes.byref(_fwd_params(**over))) == code
+
+
+def test_check_accepts_edge_values():
+    L = _lib.lib()
+    for over in ({"window": 0, "sink": 1}, {"window": 1, "sink": 0}, {"window": 10 ** 9, "sink": -3},
+                 {"softmax_scale": 0.0}, {"softmax_scale": -0.3}, {"dtype": _lib.FA_DTYPE_F16},
+                 {"head_dim": 16}, {"head_dim": 128}, {"seqlen": 1}):
+        assert L.fa_check_fwd(ctypes.byref(_fwd_params(**over))) == _lib.FA_OK, over
+
+
+@pytest.mark.parametrize("over,code", [
+    ({}, _lib.FA_OK),
+    ({"dout": None}, _lib.FA_ERR_NULL),
+    ({"dv": None}, _lib.FA_ERR_NULL),
+    ({"dq": (1 << 20) + 4}, _lib.FA_ERR_ALIGN),
+    ({"do_stride": (8 * 128 * 64, 128 * 64, 65)}, _lib.FA_ERR_ALIGN),
+    ({"head_dim": 96}, _lib.FA_ERR_HEAD_DIM),
+    ({"window": 0, "sink": 0}, _lib.FA_ERR_MASK),
+])
+def test_check_bwd_codes(over, code):
+    assert _lib.lib().fa_check_bwd(ctypes.byref(_bwd_params(**over))) == code
+
+
+def test_entry_points_reject_before_any_hip_call():
+    """fa_fwd / fa_bwd return the validation code for bad arguments (this runs without a GPU)."""
+    L = _lib.lib()
+    assert L.fa_fwd(None, None) == _lib.FA_ERR_NULL
+    assert L.fa_fwd(ctypes.byref(_fwd_params(head_dim=48)), None) == _lib.FA_ERR_HEAD_DIM
+    assert L.fa_bwd(ctypes.byref(_bwd_params(window=0, sink=0)), None, 0, None) == _lib.FA_ERR_MASK
+    # valid arguments but no workspace
+    assert L.fa_bwd(ctypes.byref(_bwd_params()), None, 0, None) == _lib.FA_ERR_WORKSPACE
+    need = L.fa_bwd_workspace_bytes(1, 8, 2, 128, 64, 16, 4)
+    assert L.fa_bwd(ctypes.byref(_bwd_params()), ctypes.c_void_p(1 << 20), need - 1, None) == _lib.FA_ERR_WORKSPACE
+    assert L.fa_bwd(ctypes.byref(_bwd_params()), ctypes.c_void_p((1 << 20) + 16), need, None) == _lib.FA_ERR_WORKSPACE
+
+
+def test_workspace_bytes():
+    L = _lib.lib()
+    ws = L.fa_bwd_workspace_bytes
+    # delta: B*Hq*round_up(L, 32) floats, 256-aligned; no sink split when every row is within
+    # the window of the sink block
+    assert ws(1, 8, 2, 128, 64, 200, 4) == 8 * 128 * 4
+    assert ws(1, 8, 2, 100, 64, 200, 4) == 8 * 128 * 4
+    # sink split: 1 block, ceil(L/256) chunks + the regular slot, dK and dV, 32 rows x D fp32
+    L_, D = 4096, 64
+    expect_delta = 64 * 4096 * 4
+    expect_partial = 8 * 1 * (16 + 1) * 2 * 32 * D * 4
+    assert ws(1, 64, 8, L_, D, 128, 4) == expect_delta + expect_partial
+    # invalid problems give 0
+    assert ws(1, 8, 3, 128, 64, 16, 4) == 0
+    assert ws(1, 8, 2, 128, 64, 0, 0) == 0
