@@ -25,6 +25,8 @@ struct Args {
   // backward workspace
   float* delta;      // [B][Hq][Lp] fp32, Lp = L rounded up to 32
   float* partial;    // sink-key partial sums, see fa_bwd.hip
+  unsigned* counters;  // per sink block arrival counters of the dK/dV kernel
+  int n_counters;
   int64_t sq[3], sk[3], sv[3], so[3], sdo[3], slse[3], sdq[3], sdk[3], sdv[3], so_out[3];
   int B, Hq, Hkv, L, G, Lp;
   int W, S;          // window and sink, clamped to [0, L]
@@ -35,8 +37,8 @@ struct Args {
   int wq, wh;
   int n_qtiles;
   // KV-major kernel (dK/dV)
-  int n_kblocks;     // ceil(L / 32)
-  int nsp;           // leading 32-key blocks whose sink rows are split into chunks
+  int n_kblocks;     // ceil(L / 64)
+  int nsp;           // leading 64-key blocks whose sink rows are split into chunks
   int n_chunks;      // chunks of chunk_rows query rows (0 when nsp == 0)
   int chunk_rows;
   int n_chunk_wgs;   // B * Hkv * nsp * n_chunks
@@ -46,6 +48,5 @@ struct Args {
 hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
 hipError_t launch_bwd_dq(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
 hipError_t launch_bwd_dkdv(const Args& a, int dtype, int D, hipStream_t stream);
-hipError_t launch_bwd_sink_finalize(const Args& a, int dtype, int D, hipStream_t stream);
 
 }  // namespace fa

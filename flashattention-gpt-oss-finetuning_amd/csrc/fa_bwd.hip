@@ -8,19 +8,16 @@
 //     dQ = scale * dS K,  dK = scale * dS^T Q,  dV = P^T dO,
 // dK/dV summed over the query heads that share a KV head.
 //
-// Three launches:
+// Two launches:
 //  1. bwd_dq_kernel (query-major, same tiling as the forward): computes delta for its rows
 //     (stored in the workspace) and dQ over the sink + window key blocks.
-//  2. bwd_dkdv_kernel (key-major): a workgroup owns 32 keys of one KV head and sweeps the
-//     (query head, 32-row query block) pairs that can see those keys; its 4 waves split that
-//     sweep and their fp32 partial sums are added in LDS in a fixed order, so the result is
-//     deterministic.  The sweep of a key block is bounded by the window: rows
-//     [k0, k0 + 31 + W).  Sink keys are also seen by every later row; those rows are split
-//     into chunks of `chunk_rows` handled by extra workgroups of the same kernel that write
-//     fp32 partial sums to the workspace (the reference instead loops one program over all
-//     of L for a sink block, benchmark_backward_speed.py:432-438).
-//  3. bwd_sink_finalize_kernel: adds the partial sums of the sink blocks in a fixed order and
-//     writes those dK/dV rows (only when some sink rows were chunked).
+//  2. bwd_dkdv_kernel (key-major): a workgroup owns 64 keys of one KV head and sweeps the
+//     (query head, 32-row query block) pairs that can see those keys, bounded by the window:
+//     rows [k0, k0 + 63 + W).  Every sum is formed in a fixed order, so results are
+//     deterministic.  Sink keys are also seen by every later row; those rows are split into
+//     chunks of `chunk_rows` handled by extra workgroups of the same kernel (the reference
+//     instead loops one program over all of L for a sink block,
+//     benchmark_backward_speed.py:432-438).
 #include "fa_args.h"
 #include "fa_common.h"
 
@@ -94,6 +91,10 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
       if (hf == 0) a.delta[(int64_t(b) * a.Hq + hw + h) * a.Lp + q] = delta[h];
     }
   }
+
+  // The dK/dV kernel's per-block arrival counters start at zero.
+  if (tile == 0)
+    for (int i = tid; i < a.n_counters; i += 256) a.counters[i] = 0u;
 
   f32x16 acc[HPW][DB];
 #pragma unroll
@@ -197,7 +198,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
           for (int e = 0; e < 16; ++e) {
             const int off = 8 * (e / 4) + (e % 4);
             float p = fast_exp2(fmaf(s[h][e], a.c, -lse2[h]));
-            if (!full && !allowed(q - kl - off, kl + off, W, S)) p = 0.f;
+            p = (full | allowed(q - kl - off, kl + off, W, S)) ? p : 0.f;
             ds[e] = p * (dp[h][e] - delta[h]);
           }
           dsb[h][0] = pack8<E>(ds);
@@ -244,58 +245,72 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// dK / dV (key-major).  Per (query head, 32-row block): S = Q K^T and dP = dO V^T in C layout
-// (lane = key column, 16 query rows per lane), then dV^T += dO^T P and dK^T += Q^T dS with
-// P/dS straight from registers and dO^T/Q^T staged per wave in LDS (permuted row order).
+// dK / dV (key-major).  A workgroup owns 64 keys of one KV head; wave (kh, hh) = (wave & 1,
+// wave >> 1) owns the 32-key half kh and takes head slot hh of every step.  A step stages two
+// (query head, 32-row block) items -- Q and dO rows plus their lse/delta -- in LDS, shared by the
+// two waves of each slot; the next step's items are fetched into registers while this step
+// computes.  Per item and wave: S = Q K^T and dP = dO V^T in C layout (lane = key column, 16
+// query rows per lane), P and dS elementwise, then dV^T += dO^T P and dK^T += Q^T dS with P/dS
+// straight from registers and dO^T/Q^T read transposed from the row-major tiles
+// (ds_read_b64_tr_b16).  The two head slots' partial sums are added in LDS at the end.
+//
+// Sink keys: for the first `nsp` blocks the rows past the window are handled by chunk
+// workgroups; every workgroup of such a block writes the fp32 partial sums of its sink rows to
+// the workspace, and the last one to arrive (a counter per block, zeroed by the dQ kernel and
+// reset by its last user) adds them in a fixed order and writes those rows.
 // ---------------------------------------------------------------------------------------------
 template <typename E, int D>
 __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   constexpr int KS = D / 16;
   constexpr int DB = D >= 32 ? D / 32 : 1;
-  constexpr int TROW = 32 + 8;                    // transposed tile row stride (elements)
-  constexpr int TILE = D * TROW;                  // one [D][32] transposed tile
-  constexpr int WAVE_LDS = 2 * TILE;              // Q^T and dO^T per wave (elements)
-  constexpr int RED_FLOATS = 3 * DB * 16 * 64;    // partial sums of waves 1..3
-  constexpr int LDS_ELEMS = (4 * WAVE_LDS > 2 * RED_FLOATS) ? 4 * WAVE_LDS : 2 * RED_FLOATS;  // uint16 units
-  constexpr int NU = (D + 63) / 64;               // transposed-load units per lane
+  constexpr int ROW = D + 8;                 // tile row stride (elements)
+  constexpr int TILE = 32 * ROW;             // 32 rows of Q or dO
+  constexpr int SLOT = 2 * TILE + 128;       // Q, dO, then lse2[32] and delta[32] as fp32
+  constexpr int STAGE = 2 * SLOT;            // two items per step
+  constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  constexpr int NCH = 2 * 2 * 32 * CPR;      // chunks per step
+  constexpr int NLD = (NCH + 255) / 256;     // chunks per thread
+  constexpr int RED = 2 * 2 * DB * 16 * 64;  // fp32 partials of the two hh = 1 waves
+  constexpr int LDS_ELEMS = (2 * STAGE > 2 * RED) ? 2 * STAGE : 2 * RED;
   __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];
+  __shared__ int last_flag;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int r32 = lane & 31, hf = lane >> 5;
+  const int kh = wave & 1, hh = wave >> 1;
   const int L = a.L, W = a.W, S = a.S, G = a.G;
 
-  // Which key block and which query rows this workgroup owns.
   int id = xcd_remap(blockIdx.x, gridDim.x);
-  int b, kvh, kblk, slot = -1, qlo, qhi;
-  bool to_partial;
+  int b, kvh, kblk, chunk = -1, qlo, qhi;
   if (id < a.n_chunk_wgs) {
-    const int c = id % a.n_chunks;
+    chunk = id % a.n_chunks;
     int t = id / a.n_chunks;
     kblk = t % a.nsp;
     t /= a.nsp;
     kvh = t % a.Hkv;
     b = t / a.Hkv;
-    qlo = kv_chunk_lo(kblk, c, a.chunk_rows, L, W);
-    qhi = kv_chunk_hi(c, a.chunk_rows, L);
-    slot = c;
-    to_partial = true;
+    qlo = kv_chunk_lo(kblk, chunk, a.chunk_rows, L, W);
+    qhi = kv_chunk_hi(chunk, a.chunk_rows, L);
   } else {
     id -= a.n_chunk_wgs;
     kblk = id % a.n_kblocks;
     const int t = id / a.n_kblocks;
     kvh = t % a.Hkv;
     b = t / a.Hkv;
-    qlo = 32 * kblk;
+    qlo = kKvKeys * kblk;
     qhi = kv_window_end(kblk, L, W);
-    to_partial = kblk < a.nsp;
-    slot = a.n_chunks;
   }
-  const int ks0 = 32 * kblk;
-  const int key = ks0 + r32;  // this lane's key column
+  const bool is_chunk = chunk >= 0;
+  const bool partial_block = kblk < a.nsp;
+  const int ks0 = kKvKeys * kblk + 32 * kh;  // this wave's keys
+  const int key = ks0 + r32;
+  const bool wave_on = ks0 < L && (!is_chunk || ks0 < S);
+  const int wqlo = is_chunk ? qlo : max(qlo, ks0), wqhi = qhi;
 
-  // K^T / V^T operands (B of S = Q K^T and dP = dO V^T): lane (key, hf) holds head-dim slice
-  // [hf*D/2 + 8ks, +8).
+  // K^T / V^T operands (B of S = Q K^T and dP = dO V^T): lane (key, hf), head-dim slice
+  // [hf*D/2 + 8ks, +8).  A negative softmax scale flips the sign of K here (exact), so scores
+  // need no per-item sign handling.
   u32x4 kf[KS], vf[KS];
   {
     const char* kp = reinterpret_cast<const char*>(a.k) +
@@ -305,7 +320,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int d = hf * (D / 2) + 8 * ks;
-      kf[ks] = key < L ? ld16(kp + 2 * d) : zero16();
+      kf[ks] = key < L ? (ld16(kp + 2 * d) ^ a.qsign) : zero16();
       vf[ks] = key < L ? ld16(vp + 2 * d) : zero16();
     }
   }
@@ -320,209 +335,273 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   const int qb_lo = qlo / 32;
   const int n_qb = qhi > qlo ? (qhi + 31) / 32 - qb_lo : 0;
   const int n_it = G * n_qb;
-  uint16_t* QT = lds + wave * WAVE_LDS;
-  uint16_t* DT = QT + TILE;
+  const int n_steps = (n_it + 1) / 2;
 
-  for (int it = wave; it < n_it; it += 4) {
-    const int hl = it / n_qb;
-    const int qb = qb_lo + it % n_qb;
-    const int h = kvh * G + hl;
-    const int qr0 = 32 * qb;
-    const int64_t qoff = int64_t(b) * a.sq[0] + int64_t(h) * a.sq[1];
-    const int64_t dooff = int64_t(b) * a.sdo[0] + int64_t(h) * a.sdo[1];
-    const char* qbase = reinterpret_cast<const char*>(a.q) + 2 * qoff;
-    const char* dobase = reinterpret_cast<const char*>(a.dout) + 2 * dooff;
+  // ---- staging of one step's two items (item it = 2*step + slot -> head it / n_qb, block
+  // it % n_qb).  The four 32-row tiles of a step (slot 0 Q, slot 0 dO, slot 1 Q, slot 1 dO) are
+  // cut into 16-byte chunks; chunk tid + 256 i sits at tile (256 i + tid) / (32 CPR), row
+  // ((256 i + tid) / CPR) % 32, column tid % CPR.  For D >= 64 the tile of every i is a
+  // compile-time constant, so the per-step address change is a uniform (scalar) offset. -------
+  static_assert(256 % CPR == 0, "chunk split");
+  const int ld_col = tid % CPR;
+  const int ld_row = (tid / CPR) & 31;
+  const char* qbase = reinterpret_cast<const char*>(a.q) + 2 * (int64_t(b) * a.sq[0] + 8 * ld_col);
+  const char* dbase = reinterpret_cast<const char*>(a.dout) + 2 * (int64_t(b) * a.sdo[0] + 8 * ld_col);
+  // per-lane row offsets (elements) of this thread's chunks
+  const int64_t qlane = int64_t(ld_row) * a.sq[2], dlane = int64_t(ld_row) * a.sdo[2];
+  const float* lsebase = a.lse + int64_t(b) * a.slse[0];
+  const float* dltbase = a.delta + int64_t(b) * a.Hq * a.Lp;
+  u32x4 stg[NLD];
+  float stat = 0.f;
+  // (item counters of the step being fetched)
+  int f_h[2], f_qb[2];
+  f_h[0] = 0;
+  f_qb[0] = 0;
+  f_h[1] = n_qb > 1 ? 0 : 1;
+  f_qb[1] = n_qb > 1 ? 1 : 0;
+  auto advance = [&]() {
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      f_qb[sl] += 2;
+      while (f_qb[sl] >= n_qb && n_qb > 0) {
+        f_qb[sl] -= n_qb;
+        ++f_h[sl];
+      }
+    }
+  };
+  auto gload = [&](int step) {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      u32x4 v = zero16();
+      if constexpr (32 * CPR >= 256) {
+        const int tile = (256 * i) / (32 * CPR);          // compile-time
+        const int slot = tile >> 1, tensor = tile & 1;
+        const int rbase = ((256 * i) / CPR) & 31;          // compile-time
+        const int it = 2 * step + slot;
+        const int qr = 32 * (qb_lo + f_qb[slot]) + rbase;  // uniform
+        if (it < n_it && qr + ld_row < L) {
+          const int h = kvh * G + f_h[slot];
+          const int64_t uoff = tensor ? int64_t(h) * a.sdo[1] + int64_t(qr) * a.sdo[2]
+                                      : int64_t(h) * a.sq[1] + int64_t(qr) * a.sq[2];
+          v = ld16((tensor ? dbase : qbase) + 2 * (uoff + (tensor ? dlane : qlane)));
+        }
+      } else {
+        const int c = tid + 256 * i;
+        const int slot = c / (2 * 32 * CPR), tensor = (c / (32 * CPR)) & 1;
+        const int row = (c / CPR) & 31;
+        const int it = 2 * step + slot;
+        const int qrow = 32 * (qb_lo + f_qb[slot]) + row;
+        if (c < NCH && it < n_it && qrow < L) {
+          const int h = kvh * G + f_h[slot];
+          const int64_t off = tensor ? int64_t(h) * a.sdo[1] + int64_t(qrow) * a.sdo[2]
+                                     : int64_t(h) * a.sq[1] + int64_t(qrow) * a.sq[2];
+          v = ld16((tensor ? dbase : qbase) + 2 * off);
+        }
+      }
+      stg[i] = v;
+    }
+    if (tid < 128) {
+      const int slot = tid >> 6, kind = (tid >> 5) & 1, row = tid & 31;
+      const int it = 2 * step + slot;
+      const int qrow = 32 * (qb_lo + f_qb[slot]) + row;
+      stat = kind ? 0.f : __builtin_inff();
+      // raw values: scaling here would make the wave wait for this load (and every load issued
+      // before it) now instead of after the compute of the current step
+      if (it < n_it && qrow < L) {
+        const int h = kvh * G + f_h[slot];
+        stat = kind ? dltbase[int64_t(h) * a.Lp + qrow] : lsebase[int64_t(h) * a.slse[1] + int64_t(qrow) * a.slse[2]];
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+    uint16_t* stage = lds + buf * STAGE;
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int c = tid + 256 * i;
+      if (c < NCH) {
+        const int slot = c / (2 * 32 * CPR), tensor = (c / (32 * CPR)) & 1;
+        const int row = (c / CPR) & 31;
+        st16(stage + slot * SLOT + tensor * TILE + row * ROW + 8 * ld_col, stg[i]);
+      }
+    }
+    if (tid < 128) {
+      const int slot = tid >> 6, kind = (tid >> 5) & 1, row = tid & 31;
+      reinterpret_cast<float*>(stage + slot * SLOT + 2 * TILE)[kind * 32 + row] = kind ? stat : stat * kLog2e;
+    }
+  };
 
-    // Stage Q^T and dO^T of rows [qr0, qr0+32) in this wave's LDS (permuted row order).
+  // Per-lane constants of the compute: LDS offsets and the mask threshold.  A key k < S is
+  // visible to every row q >= k (threshold 2^31 on the unsigned q - k); other keys to
+  // 0 <= q - k < W.
+  const int a_off = r32 * ROW + hf * (D / 2);
+  const unsigned thr = key < S ? 0x80000000u : unsigned(W);
+  // iteration counters of the item this wave computes
+  int c_h = hh < n_qb ? 0 : 1, c_qb = hh < n_qb ? hh : hh - n_qb;
+  if (n_qb == 0) c_qb = 0;
+
+  if (n_steps > 0) {
+    gload(0);
+    sstore(0);
+    advance();
+  }
+  // Nothing may be outstanding at the loop head: the compiler's wait counting is conservative
+  // across the back edge and would otherwise wait for the next step's prefetch before the first
+  // MFMA of every step.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int step = 0; step < n_steps; ++step) {
+    const bool more = step + 1 < n_steps;
+    if (more) gload(step + 1);
+    const int it = 2 * step + hh;
+    const int qr0 = 32 * (qb_lo + c_qb);
+    if (wave_on && it < n_it && qr0 + 32 > wqlo && qr0 < wqhi && kv_half_needs(qr0, ks0, L, W, S)) {
+      const uint16_t* Qt = lds + (step & 1) * STAGE + hh * SLOT;
+      const uint16_t* Dt = Qt + TILE;
+      const float* lse2 = reinterpret_cast<const float*>(Qt + 2 * TILE);
+      const float* dlt = lse2 + 32;
+      f32x16 sacc = f32x16{}, dpacc = f32x16{};
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const int unit = lane + 64 * u;
-      if (unit < D) {  // D units: 8 row quads x D/8 head-dim chunks
-        const int dc = unit % (D / 8), rq = unit / (D / 8);
-        u32x4 qr[4], dr[4];
+      for (int ks = 0; ks < KS; ++ks) {
+        sacc = E::mfma(lds16(Qt + a_off + 8 * ks), kf[ks], sacc);
+        dpacc = E::mfma(lds16(Dt + a_off + 8 * ks), vf[ks], dpacc);
+      }
+      const bool inside = qr0 >= wqlo && qr0 + 32 <= wqhi;
+      const bool full = inside && tile_full(ks0, qr0, W, S);
+      const int d0 = qr0 + 4 * hf - key;         // row - key of register e = 0
+      const int r0 = qr0 + 4 * hf - wqlo;        // row - wqlo of register e = 0
+      const unsigned span = unsigned(wqhi - wqlo);
+      float p[16], ds[16];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = qr0 + 4 * rq + r;
-          qr[r] = zero16();
-          dr[r] = zero16();
-          if (row < L) {
-            qr[r] = ld16(qbase + 2 * (int64_t(row) * a.sq[2] + 8 * dc));
-            dr[r] = ld16(dobase + 2 * (int64_t(row) * a.sdo[2] + 8 * dc));
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2 + 8 * j + 4 * hf);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlt + 8 * j + 4 * hf);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = 4 * j + i, off = 8 * j + i;
+          float pe = fast_exp2(fmaf(sacc[e], a.c, -l4[i]));
+          if (!full) {
+            bool ok = unsigned(d0 + off) < thr;
+            if (!inside) ok &= unsigned(r0 + off) < span;
+            pe = ok ? pe : 0.f;
           }
-        }
-        u32x2 qc[8], dc8[8];
-        transpose4x8(qr, qc);
-        transpose4x8(dr, dc8);
-        const int pos = perm_pos(4 * rq);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          *reinterpret_cast<u32x2*>(QT + (8 * dc + i) * TROW + pos) = qc[i];
-          *reinterpret_cast<u32x2*>(DT + (8 * dc + i) * TROW + pos) = dc8[i];
+          p[e] = pe;
+          ds[e] = pe * (dpacc[e] - d4[i]);
         }
       }
-    }
-
-    // Row operands Q, dO (A of S and dP): lane (row qr0 + r32, hf).
-    const int arow = qr0 + r32;
-    u32x4 qa[KS], da[KS];
+      const u32x4 pb0 = pack8<E>(p), pb1 = pack8<E>(p + 8);
+      const u32x4 sb0 = pack8<E>(ds), sb1 = pack8<E>(ds + 8);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int d = hf * (D / 2) + 8 * ks;
-      qa[ks] = zero16();
-      da[ks] = zero16();
-      if (arow < L) {
-        qa[ks] = ld16(qbase + 2 * (int64_t(arow) * a.sq[2] + d));
-        da[ks] = ld16(dobase + 2 * (int64_t(arow) * a.sdo[2] + d));
-      }
-      qa[ks] ^= a.qsign;
-    }
-    // Row statistics of the 16 rows this lane holds in C layout: qr0 + 8j + 4hf + (0..3).
-    float l2[16], dl[16];
-    const float* lsep = a.lse + int64_t(b) * a.slse[0] + int64_t(h) * a.slse[1];
-    const float* dlp = a.delta + (int64_t(b) * a.Hq + h) * a.Lp;
+      for (int db = 0; db < DB; ++db) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r0 = qr0 + 8 * j + 4 * hf;
-      const f32x4 dq4 = *reinterpret_cast<const f32x4*>(dlp + r0);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = r0 + e;
-        l2[4 * j + e] = row < L ? lsep[int64_t(row) * a.slse[2]] * kLog2e : __builtin_inff();
-        dl[4 * j + e] = row < L ? dq4[e] : 0.f;
-      }
-    }
-
-    f32x16 s = f32x16{}, dp = f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      s = E::mfma(qa[ks], kf[ks], s);
-      dp = E::mfma(da[ks], vf[ks], dp);
-    }
-    // Rows outside [qlo, qhi) belong to another workgroup; rows/keys outside the mask are 0.
-    const bool full = (qr0 >= qlo) && (qr0 + 32 <= qhi) && tile_full(ks0, qr0, W, S);
-    float p[16], ds[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int row = qr0 + 8 * (e / 4) + 4 * hf + (e % 4);
-      float pe = fast_exp2(fmaf(s[e], a.c, -l2[e]));
-      if (!full && !(row >= qlo && row < qhi && allowed(row - key, key, W, S))) pe = 0.f;
-      p[e] = pe;
-      ds[e] = pe * (dp[e] - dl[e]);
-    }
-    const u32x4 pb0 = pack8<E>(p), pb1 = pack8<E>(p + 8);
-    const u32x4 sb0 = pack8<E>(ds), sb1 = pack8<E>(ds + 8);
-    const int trow = sigma32(r32);
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        u32x4 dt = zero16(), qt = zero16();
-        if (D >= 32 || trow < D) {
-          const int off = (32 * db + trow) * TROW + 16 * t + 8 * hf;
-          dt = *reinterpret_cast<const u32x4*>(DT + off);
-          qt = *reinterpret_cast<const u32x4*>(QT + off);
+        for (int t = 0; t < 2; ++t) {
+          const u32x4 dt = tr_frag<ROW>(Dt, 16 * t, 32 * db, D);
+          const u32x4 qt = tr_frag<ROW>(Qt, 16 * t, 32 * db, D);
+          dv[db] = E::mfma(dt, t ? pb1 : pb0, dv[db]);
+          dk[db] = E::mfma(qt, t ? sb1 : sb0, dk[db]);
         }
-        dv[db] = E::mfma(dt, t ? pb1 : pb0, dv[db]);
-        dk[db] = E::mfma(qt, t ? sb1 : sb0, dk[db]);
       }
     }
+    // next item of this wave's slot
+    c_qb += 2;
+    while (c_qb >= n_qb && n_qb > 0) {
+      c_qb -= n_qb;
+      ++c_h;
+    }
+    if (more) {
+      sstore((step + 1) & 1);
+      advance();
+    }
+    __syncthreads();
   }
 
-  // Fixed-order reduction of the 4 waves' partial sums (wave 0 + 1 + 2 + 3), dK then dV.
+  // ---- add the two head slots' partial sums (hh = 0 gets hh = 1's), fixed order ---------------
   float* red = reinterpret_cast<float*>(lds);
+  if (hh == 1) {
 #pragma unroll
-  for (int part = 0; part < 2; ++part) {
-    f32x16* x = part ? dv : dk;
-    __syncthreads();
-    if (wave > 0) {
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) red[(((wave - 1) * DB + db) * 16 + e) * 64 + lane] = x[db][e];
-    }
-    __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-#pragma unroll
-          for (int w = 0; w < 3; ++w) x[db][e] += red[((w * DB + db) * 16 + e) * 64 + lane];
-    }
+      for (int e = 0; e < 16; ++e) {
+        red[((kh * 2 + 0) * DB * 16 + db * 16 + e) * 64 + lane] = dk[db][e];
+        red[((kh * 2 + 1) * DB * 16 + db * 16 + e) * 64 + lane] = dv[db][e];
+      }
   }
-  if (wave != 0) return;
+  __syncthreads();
+  if (hh == 0) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        dk[db][e] += red[((kh * 2 + 0) * DB * 16 + db * 16 + e) * 64 + lane];
+        dv[db][e] += red[((kh * 2 + 1) * DB * 16 + db * 16 + e) * 64 + lane];
+      }
+  }
 
-  // Lane (key, hf) owns head-dim indices 32db + 16hf + e (D == 16: hf == 0 only).
-  if (to_partial) {
-    float* pk = a.partial + ((((int64_t(b) * a.Hkv + kvh) * a.nsp + kblk) * (a.n_chunks + 1) + slot) * 2) * 32 * D;
-    float* pv = pk + 32 * D;
+  // ---- outputs: lane (key, hf) holds head-dim indices 32db + 16hf + e (D == 16: hf == 0) ------
+  float* pk = nullptr;
+  if (partial_block) {
+    const int64_t blk = (int64_t(b) * a.Hkv + kvh) * a.nsp + kblk;
+    const int slot = is_chunk ? chunk : a.n_chunks;
+    pk = a.partial + (blk * (a.n_chunks + 1) + slot) * 2 * kKvKeys * D;
+  }
+  if (hh == 0 && key < L) {
+    const bool sink_row = partial_block && key < S;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       if (D == 16 && hf == 1) continue;
       const int d0 = 32 * db + (D >= 32 ? 16 * hf : 0);
+      if (sink_row) {
+        float* rk = pk + (32 * kh + r32) * D + d0;
+        float* rv = rk + kKvKeys * D;
 #pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        *reinterpret_cast<f32x4*>(pk + r32 * D + d0 + 4 * e4) =
-            f32x4{dk[db][4 * e4], dk[db][4 * e4 + 1], dk[db][4 * e4 + 2], dk[db][4 * e4 + 3]};
-        *reinterpret_cast<f32x4*>(pv + r32 * D + d0 + 4 * e4) =
-            f32x4{dv[db][4 * e4], dv[db][4 * e4 + 1], dv[db][4 * e4 + 2], dv[db][4 * e4 + 3]};
+        for (int e4 = 0; e4 < 4; ++e4) {
+          *reinterpret_cast<f32x4*>(rk + 4 * e4) =
+              f32x4{dk[db][4 * e4], dk[db][4 * e4 + 1], dk[db][4 * e4 + 2], dk[db][4 * e4 + 3]};
+          *reinterpret_cast<f32x4*>(rv + 4 * e4) =
+              f32x4{dv[db][4 * e4], dv[db][4 * e4 + 1], dv[db][4 * e4 + 2], dv[db][4 * e4 + 3]};
+        }
+      } else if (!is_chunk) {
+        char* dkp = reinterpret_cast<char*>(a.dk) +
+                    2 * (int64_t(b) * a.sdk[0] + int64_t(kvh) * a.sdk[1] + int64_t(key) * a.sdk[2]);
+        char* dvp = reinterpret_cast<char*>(a.dv) +
+                    2 * (int64_t(b) * a.sdv[0] + int64_t(kvh) * a.sdv[1] + int64_t(key) * a.sdv[2]);
+        float kv[16], vv[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          kv[e] = dk[db][e] * a.scale;
+          vv[e] = dv[db][e];
+        }
+        st16(dkp + 2 * d0, pack8<E>(kv));
+        st16(dkp + 2 * (d0 + 8), pack8<E>(kv + 8));
+        st16(dvp + 2 * d0, pack8<E>(vv));
+        st16(dvp + 2 * (d0 + 8), pack8<E>(vv + 8));
       }
     }
-    return;
   }
-  if (key >= L) return;
-  char* dkp = reinterpret_cast<char*>(a.dk) +
-              2 * (int64_t(b) * a.sdk[0] + int64_t(kvh) * a.sdk[1] + int64_t(key) * a.sdk[2]);
-  char* dvp = reinterpret_cast<char*>(a.dv) +
-              2 * (int64_t(b) * a.sdv[0] + int64_t(kvh) * a.sdv[1] + int64_t(key) * a.sdv[2]);
-#pragma unroll
-  for (int db = 0; db < DB; ++db) {
-    if (D == 16 && hf == 1) continue;
-    float kv[16], vv[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      kv[e] = dk[db][e] * a.scale;
-      vv[e] = dv[db][e];
-    }
-    const int d0 = 32 * db + (D >= 32 ? 16 * hf : 0);
-    st16(dkp + 2 * d0, pack8<E>(kv));
-    st16(dkp + 2 * (d0 + 8), pack8<E>(kv + 8));
-    st16(dvp + 2 * d0, pack8<E>(vv));
-    st16(dvp + 2 * (d0 + 8), pack8<E>(vv + 8));
-  }
-}
+  if (!partial_block) return;
 
-// ---------------------------------------------------------------------------------------------
-// Sink finalize: dK/dV rows of the chunked sink blocks = fixed-order sum of their partials.
-// One thread per (b, kvh, block, row, head-dim index).
-// ---------------------------------------------------------------------------------------------
-template <typename E, int D>
-__global__ __launch_bounds__(256) void bwd_sink_finalize_kernel(const Args a) {
-  const int64_t n = int64_t(a.B) * a.Hkv * a.nsp * 32 * D;
-  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= n) return;
-  const int d = int(i % D);
-  const int row = int((i / D) % 32);
-  const int64_t blk = i / (int64_t(32) * D);  // (b*Hkv + kvh)*nsp + kblk
-  const int kblk = int(blk % a.nsp);
-  const int kvh = int((blk / a.nsp) % a.Hkv);
-  const int b = int(blk / (int64_t(a.nsp) * a.Hkv));
-  const int key = 32 * kblk + row;
-  if (key >= a.L) return;
-  const float* base = a.partial + blk * (a.n_chunks + 1) * 2 * 32 * D + row * D + d;
-  float sk = 0.f, sv = 0.f;
-  for (int s = 0; s <= a.n_chunks; ++s) {
-    sk += base[int64_t(s) * 2 * 32 * D];
-    sv += base[int64_t(s) * 2 * 32 * D + 32 * D];
+  // ---- last workgroup of a sink block: fixed-order sum of the n_chunks + 1 partials -----------
+  __threadfence();
+  __syncthreads();
+  const int64_t blk = (int64_t(b) * a.Hkv + kvh) * a.nsp + kblk;
+  if (tid == 0) last_flag = atomicAdd(&a.counters[blk], 1u) == unsigned(a.n_chunks);
+  __syncthreads();
+  if (!last_flag) return;
+  __threadfence();
+  const int nrows = min(kKvKeys, min(S, L) - kKvKeys * kblk);
+  const float* base = a.partial + blk * (a.n_chunks + 1) * 2 * kKvKeys * D;
+  for (int i = tid; i < 2 * nrows * D; i += 256) {
+    const int part = i / (nrows * D), rem = i % (nrows * D);
+    const int row = rem / D, d = rem % D;
+    const float* src = base + part * kKvKeys * D + row * D + d;
+    float sum = 0.f;
+    for (int sl = 0; sl <= a.n_chunks; ++sl) sum += src[int64_t(sl) * 2 * kKvKeys * D];
+    const int k2 = kKvKeys * kblk + row;
+    uint16_t* dst = reinterpret_cast<uint16_t*>(part ? a.dv : a.dk) +
+                    int64_t(b) * (part ? a.sdv[0] : a.sdk[0]) + int64_t(kvh) * (part ? a.sdv[1] : a.sdk[1]) +
+                    int64_t(k2) * (part ? a.sdv[2] : a.sdk[2]) + d;
+    *dst = uint16_t(E::pack2(part ? sum : sum * a.scale, 0.f));
   }
-  sk *= a.scale;
-  uint16_t* dkp = reinterpret_cast<uint16_t*>(a.dk) + int64_t(b) * a.sdk[0] + int64_t(kvh) * a.sdk[1] +
-                  int64_t(key) * a.sdk[2] + d;
-  uint16_t* dvp = reinterpret_cast<uint16_t*>(a.dv) + int64_t(b) * a.sdv[0] + int64_t(kvh) * a.sdv[1] +
-                  int64_t(key) * a.sdv[2] + d;
-  const uint32_t pk = E::pack2(sk, sv);
-  *dkp = uint16_t(pk);
-  *dvp = uint16_t(pk >> 16);
+  if (tid == 0) a.counters[blk] = 0u;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -542,14 +621,6 @@ static hipError_t launch_dkdv_d(const Args& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <typename E, int D>
-static hipError_t launch_fin_d(const Args& a, hipStream_t stream) {
-  const int64_t n = int64_t(a.B) * a.Hkv * a.nsp * 32 * D;
-  const dim3 grid(unsigned((n + 255) / 256)), block(256);
-  hipLaunchKernelGGL((bwd_sink_finalize_kernel<E, D>), grid, block, 0, stream, a);
-  return hipGetLastError();
-}
-
 #define FA_DISPATCH_D(FN, E, D, ...)                          \
   switch (D) {                                                \
     case 16: return FN<E, 16>(__VA_ARGS__);                   \
@@ -563,17 +634,12 @@ template <typename E>
 static hipError_t dq_e(const Args& a, int D, int hpw, hipStream_t s) { FA_DISPATCH_D(launch_dq_d, E, D, a, hpw, s) }
 template <typename E>
 static hipError_t dkdv_e(const Args& a, int D, hipStream_t s) { FA_DISPATCH_D(launch_dkdv_d, E, D, a, s) }
-template <typename E>
-static hipError_t fin_e(const Args& a, int D, hipStream_t s) { FA_DISPATCH_D(launch_fin_d, E, D, a, s) }
 
 hipError_t launch_bwd_dq(const Args& a, int dtype, int D, int hpw, hipStream_t s) {
   return dtype == 1 ? dq_e<BF16>(a, D, hpw, s) : dq_e<F16>(a, D, hpw, s);
 }
 hipError_t launch_bwd_dkdv(const Args& a, int dtype, int D, hipStream_t s) {
   return dtype == 1 ? dkdv_e<BF16>(a, D, s) : dkdv_e<F16>(a, D, s);
-}
-hipError_t launch_bwd_sink_finalize(const Args& a, int dtype, int D, hipStream_t s) {
-  return dtype == 1 ? fin_e<BF16>(a, D, s) : fin_e<F16>(a, D, s);
 }
 
 }  // namespace fa

@@ -84,7 +84,11 @@ size_t delta_bytes(int B, int Hq, int L) {
 }
 
 size_t partial_bytes(int B, int Hkv, int D, const SinkPlan& sp) {
-  return align256(size_t(B) * Hkv * sp.nsp * (sp.n_chunks + 1) * 2 * 32 * D * sizeof(float));
+  return align256(size_t(B) * Hkv * sp.nsp * (sp.n_chunks + 1) * 2 * fa::kKvKeys * D * sizeof(float));
+}
+
+size_t counter_bytes(int B, int Hkv, const SinkPlan& sp) {
+  return align256(size_t(B) * Hkv * sp.nsp * sizeof(unsigned));
 }
 
 void copy3(int64_t dst[3], const int64_t src[3]) {
@@ -179,7 +183,8 @@ size_t fa_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t heads_kv, 
   if (check_common(batch, heads_q, heads_kv, seqlen, head_dim, window, sink, 1.f, FA_DTYPE_BF16) != FA_OK)
     return 0;
   const SinkPlan sp = sink_plan(seqlen, window, sink);
-  return delta_bytes(batch, heads_q, seqlen) + partial_bytes(batch, heads_kv, head_dim, sp);
+  return delta_bytes(batch, heads_q, seqlen) + partial_bytes(batch, heads_kv, head_dim, sp) +
+         counter_bytes(batch, heads_kv, sp);
 }
 
 }  // extern "C"
@@ -215,7 +220,6 @@ int prepare_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
   copy3(a.sdk, p->dk_stride);
   copy3(a.sdv, p->dv_stride);
   a.delta = static_cast<float*>(workspace);
-  a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + delta_bytes(a.B, a.Hq, a.L));
 
   int wh, wq;
   choose_qmajor(a.G, p->head_dim, hpw, &wh, &wq);
@@ -224,7 +228,11 @@ int prepare_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
   a.n_qtiles = (a.L + 32 * wq - 1) / (32 * wq);
 
   const SinkPlan sp = sink_plan(a.L, p->window, p->sink);
-  a.n_kblocks = (a.L + 31) / 32;
+  char* ws = static_cast<char*>(workspace);
+  a.partial = reinterpret_cast<float*>(ws + delta_bytes(a.B, a.Hq, a.L));
+  a.counters = reinterpret_cast<unsigned*>(ws + delta_bytes(a.B, a.Hq, a.L) + partial_bytes(a.B, a.Hkv, p->head_dim, sp));
+  a.n_counters = a.B * a.Hkv * sp.nsp;
+  a.n_kblocks = (a.L + fa::kKvKeys - 1) / fa::kKvKeys;
   a.nsp = sp.nsp;
   a.n_chunks = sp.n_chunks;
   a.chunk_rows = kChunkRows;
@@ -238,9 +246,7 @@ int run_dq(const fa::Args& a, const fa_bwd_params* p, int hpw, hipStream_t s) {
 }
 
 int run_dkdv(const fa::Args& a, const fa_bwd_params* p, hipStream_t s) {
-  if (fa::launch_bwd_dkdv(a, p->dtype, p->head_dim, s) != hipSuccess) return FA_ERR_LAUNCH;
-  if (a.nsp > 0 && fa::launch_bwd_sink_finalize(a, p->dtype, p->head_dim, s) != hipSuccess) return FA_ERR_LAUNCH;
-  return FA_OK;
+  return fa::launch_bwd_dkdv(a, p->dtype, p->head_dim, s) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 
 }  // namespace

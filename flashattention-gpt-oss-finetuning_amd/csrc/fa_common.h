@@ -107,6 +107,35 @@ __device__ __forceinline__ int sigma32(int m) { return ((m >> 2) & 1) * 16 + (m 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ u32x4 zero16() { return u32x4{0u, 0u, 0u, 0u}; }
+__device__ __forceinline__ u32x4 lds16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, output lane i, element j is
+// element (i & 3) of the 8 bytes addressed by lane 4j + (i >> 2) of the group.  (Checked on
+// hardware by an in-bounds probe.)  Reading 4 rows x 16 columns of a row-major LDS tile this way
+// hands each lane one column and 4 consecutive rows: a transposed read with no extra LDS copy.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t* p) {
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// A operand of v_mfma_f32_32x32x16 whose rows are head-dim indices and whose reduction index
+// runs over tile rows, read from a row-major LDS tile [rows][ROW] (16-bit elements):
+// lane (r = lane % 32, h = lane / 32) receives column col0 + sigma32(r) of tile rows
+// {r0 + 4h + 0..3, r0 + 8 + 4h + 0..3} -- the row order of a C tile fed back as B operand.
+// `ncols` columns exist; lanes whose column is >= ncols get zeros (only D = 16 has such lanes).
+template <int ROW>
+__device__ __forceinline__ u32x4 tr_frag(const uint16_t* tile, int r0, int col0, int ncols) {
+  const int lane = threadIdx.x & 63;
+  const int s = lane & 15, rh = (lane >> 4) & 1, hf = lane >> 5;
+  int col = col0 + sigma32(16 * rh + 4 * (s & 3));
+  if (col >= ncols) col = 0;  // any valid address; those lanes are zeroed below
+  const uint16_t* p = tile + (r0 + 4 * hf + (s >> 2)) * ROW + col;
+  const u32x2 lo = ds_read_tr16(p), hi = ds_read_tr16(p + 8 * ROW);
+  u32x4 r = {lo[0], lo[1], hi[0], hi[1]};
+  if (col0 + sigma32(lane & 31) >= ncols) r = zero16();
+  return r;
+}
 
 // Exchange with the lane 32 positions away (the other half of the wave).
 __device__ __forceinline__ float xor32(float x) {

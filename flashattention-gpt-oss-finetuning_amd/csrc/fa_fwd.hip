@@ -164,7 +164,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
               const int off = 8 * (e / 4) + (e % 4);
-              if (!allowed(q - kl - off, kl + off, W, S)) sv[e] = kNegInf;
+              sv[e] = allowed(q - kl - off, kl + off, W, S) ? sv[e] : kNegInf;
             }
           }
           float mx = sv[0];

@@ -23,8 +23,8 @@ constexpr int kStep = 32;     // keys (or query rows) per MFMA tile edge
 FA_HD int imin(int a, int b) { return a < b ? a : b; }
 FA_HD int imax(int a, int b) { return a > b ? a : b; }
 
-// dq = q - k
-FA_HD bool allowed(int dq, int k, int W, int S) { return dq >= 0 && (dq < W || k < S); }
+// dq = q - k.  Bitwise operators (no short-circuit), so the kernels get selects, not branches.
+FA_HD bool allowed(int dq, int k, int W, int S) { return (dq >= 0) & ((dq < W) | (k < S)); }
 
 // ---- query-major kernels (forward, dQ) --------------------------------------------------------
 // A workgroup owns rows [q0, q0 + bm).  It visits, in LDS blocks of 64 keys, the sink blocks
@@ -62,12 +62,25 @@ FA_HD bool tile_full(int ks0, int qr, int W, int S) {
 }
 
 // ---- key-major kernel (dK, dV) ----------------------------------------------------------------
-// Key block kblk = keys [32 kblk, 32 kblk + 32).  Its regular workgroup covers rows
-// [32 kblk, kv_window_end): every window pair of the block lies there.  For the first `nsp`
-// blocks (those holding sink keys with rows beyond kv_window_end) the remaining rows
-// [kv_window_end, L) only see the sink keys; they are split into chunks of chunk_rows handled by
-// extra workgroups, chunk c covering [max(c*chunk_rows, end), min((c+1)*chunk_rows, L)).
-FA_HD int kv_window_end(int kblk, int L, int W) { return imin(L, kStep * kblk + kStep - 1 + W); }
+// A workgroup owns the kKvKeys keys [kKvKeys*kblk, +kKvKeys); each of its waves owns a 32-key
+// half.  The rows that can see a 32-key half [ks0, ks0 + 32) through the window are
+// [ks0, ks0 + 31 + W); the workgroup sweeps the union of its halves' ranges,
+// [kKvKeys*kblk, kv_window_end), each wave from its own first key on (a half's sink keys are
+// also seen by the rows between its own window end and the workgroup's).  For the first `nsp` blocks (those holding sink keys with
+// rows beyond kv_window_end) the remaining rows [kv_window_end, L) only see the sink keys;
+// they are split into chunks of chunk_rows handled by extra workgroups, chunk c covering
+// [max(c*chunk_rows, end), min((c+1)*chunk_rows, L)).
+constexpr int kKvKeys = 64;
+
+FA_HD int kv_rows_end(int ks0, int nkeys, int L, int W) { return imin(L, ks0 + nkeys - 1 + W); }
+
+FA_HD int kv_window_end(int kblk, int L, int W) { return kv_rows_end(kKvKeys * kblk, kKvKeys, L, W); }
+
+// Does the wave owning keys [ks0, ks0 + 32) have any allowed pair with rows [qr0, qr0 + 32)?
+// Rows past the half's window only see its sink keys.
+FA_HD bool kv_half_needs(int qr0, int ks0, int L, int W, int S) {
+  return qr0 + 31 >= ks0 && (ks0 < S || qr0 < kv_rows_end(ks0, 32, L, W));
+}
 
 FA_HD int kv_chunk_lo(int kblk, int c, int chunk_rows, int L, int W) {
   return imax(c * chunk_rows, kv_window_end(kblk, L, W));
@@ -79,7 +92,7 @@ FA_HD int kv_chunk_hi(int c, int chunk_rows, int L) { return imin((c + 1) * chun
 // window end is before L.  (Both conditions hold on a prefix of the blocks.)
 FA_HD int kv_sink_blocks(int L, int W, int S) {
   int n = 0;
-  for (int kb = 0; kStep * kb < S; ++kb)
+  for (int kb = 0; kKvKeys * kb < S; ++kb)
     if (kv_window_end(kb, L, W) < L) n = kb + 1;
   return n;
 }

@@ -61,38 +61,49 @@ static int check_qmajor(int L, int W, int S, int wq) {
   return 0;
 }
 
-// Key-major: regular workgroups per 32-key block, plus chunk workgroups for the sink blocks.
+// Key-major: regular workgroups per kKvKeys-key block (waves per 32-key half), plus chunk
+// workgroups for the sink blocks.  A wave sweeps the workgroup's rows from its own first key on,
+// skipping q-blocks that kv_half_needs rules out, and, in a chunk workgroup, halves without sink
+// keys.
 static int check_kvmajor(int L, int W, int S, int chunk_rows) {
   std::vector<int> cnt(size_t(L) * L, 0);
-  const int nkb = (L + 31) / 32;
+  const int nkb = (L + kKvKeys - 1) / kKvKeys;
   const int nsp = kv_sink_blocks(L, W, S);
   const int n_chunks = nsp > 0 ? (L + chunk_rows - 1) / chunk_rows : 0;
-  auto sweep = [&](int kblk, int qlo, int qhi) -> int {
-    const int ks0 = 32 * kblk;
+  auto sweep = [&](int kblk, int qlo, int qhi, bool chunk) -> int {
     if (qhi <= qlo) return 0;
     for (int qb = qlo / 32; qb < (qhi + 31) / 32; ++qb) {
       const int qr0 = 32 * qb;
-      const bool full = (qr0 >= qlo) && (qr0 + 32 <= qhi) && tile_full(ks0, qr0, W, S);
-      for (int r = 0; r < 32; ++r)
-        for (int c = 0; c < 32; ++c) {
-          const int q = qr0 + r, k = ks0 + c;
-          const bool ok = full || (q >= qlo && q < qhi && allowed(q - k, k, W, S));
-          if (!ok) continue;
-          if (q >= L || k >= L) {
-            if (full) return fail("full kv tile beyond L", L, W, S, chunk_rows, q, k, 0);
-            return fail("kv pair beyond L passes", L, W, S, chunk_rows, q, k, 0);
+      for (int kh = 0; kh < kKvKeys / 32; ++kh) {
+        const int ks0 = kKvKeys * kblk + 32 * kh;
+        if (ks0 >= L) continue;
+        if (chunk && ks0 >= S) continue;
+        const int hqlo = chunk ? qlo : imax(qlo, ks0);
+        const int hqhi = qhi;
+        if (qr0 + 32 <= hqlo || qr0 >= hqhi) continue;  // q-block outside this half's rows
+        if (!kv_half_needs(qr0, ks0, L, W, S)) continue;  // beyond the half's window, no sinks
+        const bool full = (qr0 >= hqlo) && (qr0 + 32 <= hqhi) && tile_full(ks0, qr0, W, S);
+        for (int r = 0; r < 32; ++r)
+          for (int c = 0; c < 32; ++c) {
+            const int q = qr0 + r, k = ks0 + c;
+            const bool ok = full || (q >= hqlo && q < hqhi && allowed(q - k, k, W, S));
+            if (!ok) continue;
+            if (q >= L || k >= L) {
+              if (full) return fail("full kv tile beyond L", L, W, S, chunk_rows, q, k, 0);
+              return fail("kv pair beyond L passes", L, W, S, chunk_rows, q, k, 0);
+            }
+            if (full && !ref_allowed(q, k, W, S)) return fail("full kv tile has a masked pair", L, W, S, chunk_rows, q, k, 0);
+            ++cnt[size_t(q) * L + k];
           }
-          if (full && !ref_allowed(q, k, W, S)) return fail("full kv tile has a masked pair", L, W, S, chunk_rows, q, k, 0);
-          ++cnt[size_t(q) * L + k];
-        }
+      }
     }
     return 0;
   };
   for (int kblk = 0; kblk < nkb; ++kblk)
-    if (sweep(kblk, 32 * kblk, kv_window_end(kblk, L, W))) return 1;
+    if (sweep(kblk, kKvKeys * kblk, kv_window_end(kblk, L, W), false)) return 1;
   for (int kblk = 0; kblk < nsp; ++kblk)
     for (int c = 0; c < n_chunks; ++c)
-      if (sweep(kblk, kv_chunk_lo(kblk, c, chunk_rows, L, W), kv_chunk_hi(c, chunk_rows, L))) return 1;
+      if (sweep(kblk, kv_chunk_lo(kblk, c, chunk_rows, L, W), kv_chunk_hi(c, chunk_rows, L), true)) return 1;
   for (int q = 0; q < L; ++q)
     for (int k = 0; k < L; ++k) {
       const int want = ref_allowed(q, k, W, S) ? 1 : 0;
