@@ -18,6 +18,8 @@
 //     chunks of `chunk_rows` handled by extra workgroups of the same kernel (the reference
 //     instead loops one program over all of L for a sink block,
 //     benchmark_backward_speed.py:432-438).
+#include <type_traits>
+
 #include "fa_args.h"
 #include "fa_common.h"
 
@@ -332,185 +334,196 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
     dv[db] = f32x16{};
   }
 
+  // Items: (query head h, 32-row block qb) for h < G and qb < n_qb.  Step (h, qp) stages the
+  // two items (h, 2qp) and (h, 2qp + 1) -- slot 0 and slot 1 -- so a step never spans two heads.
   const int qb_lo = qlo / 32;
   const int n_qb = qhi > qlo ? (qhi + 31) / 32 - qb_lo : 0;
-  const int n_it = G * n_qb;
-  const int n_steps = (n_it + 1) / 2;
+  const int n_qp = (n_qb + 1) / 2;
+  const int n_steps = G * n_qp;
 
-  // ---- staging of one step's two items (item it = 2*step + slot -> head it / n_qb, block
-  // it % n_qb).  The four 32-row tiles of a step (slot 0 Q, slot 0 dO, slot 1 Q, slot 1 dO) are
-  // cut into 16-byte chunks; chunk tid + 256 i sits at tile (256 i + tid) / (32 CPR), row
-  // ((256 i + tid) / CPR) % 32, column tid % CPR.  For D >= 64 the tile of every i is a
-  // compile-time constant, so the per-step address change is a uniform (scalar) offset. -------
-  static_assert(256 % CPR == 0, "chunk split");
-  const int ld_col = tid % CPR;
-  const int ld_row = (tid / CPR) & 31;
-  const char* qbase = reinterpret_cast<const char*>(a.q) + 2 * (int64_t(b) * a.sq[0] + 8 * ld_col);
-  const char* dbase = reinterpret_cast<const char*>(a.dout) + 2 * (int64_t(b) * a.sdo[0] + 8 * ld_col);
-  // per-lane row offsets (elements) of this thread's chunks
-  const int64_t qlane = int64_t(ld_row) * a.sq[2], dlane = int64_t(ld_row) * a.sdo[2];
-  const float* lsebase = a.lse + int64_t(b) * a.slse[0];
-  const float* dltbase = a.delta + int64_t(b) * a.Hq * a.Lp;
-  u32x4 stg[NLD];
-  float stat = 0.f;
-  // (item counters of the step being fetched)
-  int f_h[2], f_qb[2];
-  f_h[0] = 0;
-  f_qb[0] = 0;
-  f_h[1] = n_qb > 1 ? 0 : 1;
-  f_qb[1] = n_qb > 1 ? 1 : 0;
-  auto advance = [&]() {
+  // ---- staging.  The four 32-row tiles of a step (slot 0 Q, slot 0 dO, slot 1 Q, slot 1 dO)
+  // are loaded through buffer resources spanning one query head's rows [0, L) (rows past L read
+  // as zero; a head slice is < 2^31 bytes, checked by the C ABI).  Descriptors change only with
+  // the head; a step adds its block offset to loop-invariant per-lane offsets.  Load i handles
+  // tile i / ITPT (compile-time) and chunk (i % ITPT) * 256 + tid of it. ------------------------
+  constexpr int TPI = 32 * CPR;                  // 16-byte chunks per tile
+  constexpr int ITPT = TPI >= 256 ? TPI / 256 : 1;
+  constexpr bool ALL_ON = TPI >= 256;            // every thread loads a chunk of every tile
+  constexpr int NL = 4 * ITPT;
+  uint32_t lane_off_q[ITPT], lane_off_d[ITPT];
+  int lane_lds[ITPT];
+  bool lane_on[ITPT];
 #pragma unroll
-    for (int sl = 0; sl < 2; ++sl) {
-      f_qb[sl] += 2;
-      while (f_qb[sl] >= n_qb && n_qb > 0) {
-        f_qb[sl] -= n_qb;
-        ++f_h[sl];
-      }
+  for (int i = 0; i < ITPT; ++i) {
+    const int wc = i * 256 + tid;
+    const int row = wc / CPR, col = wc % CPR;
+    lane_on[i] = ALL_ON || wc < TPI;
+    lane_off_q[i] = uint32_t((int64_t(row) * a.sq[2] + 8 * col) * 2);
+    lane_off_d[i] = uint32_t((int64_t(row) * a.sdo[2] + 8 * col) * 2);
+    lane_lds[i] = row * ROW + 8 * col;
+  }
+  const char* qslice = reinterpret_cast<const char*>(a.q) + 2 * (int64_t(b) * a.sq[0] + int64_t(kvh) * G * a.sq[1]);
+  const char* dslice = reinterpret_cast<const char*>(a.dout) + 2 * (int64_t(b) * a.sdo[0] + int64_t(kvh) * G * a.sdo[1]);
+  const char* lslice = reinterpret_cast<const char*>(a.lse + int64_t(b) * a.slse[0] + int64_t(kvh) * G * a.slse[1]);
+  const char* tslice = reinterpret_cast<const char*>(a.delta + (int64_t(b) * a.Hq + int64_t(kvh) * G) * a.Lp);
+  const uint32_t nq = span_bytes(L, a.sq[2], D), nd = span_bytes(L, a.sdo[2], D);
+  const uint32_t nl = uint32_t((int64_t(L - 1) * a.slse[2] + 1) * 4), nt = uint32_t(L * 4);
+  // bytes per 32-row block
+  const uint32_t bq = uint32_t(64 * a.sq[2]), bd = uint32_t(64 * a.sdo[2]), bl = uint32_t(128 * a.slse[2]);
+  // stats: thread tid < 128 loads row tid % 32 of (slot tid / 64, kind (tid / 32) % 2).  Every
+  // thread issues both loads (threads >= 128 at an offset past any buffer, which reads 0), so
+  // the number of loads in flight is the same on every path.
+  const int st_slot = (tid >> 6) & 1, st_kind = (tid >> 5) & 1, st_row = tid & 31;
+  const uint32_t st_far = tid < 128 ? 0u : 0x80000000u;
+  const uint32_t lse_off = uint32_t(int64_t(st_row) * 4 * a.slse[2]) | st_far, dlt_off = uint32_t(st_row * 4) | st_far;
+  // Register staging of one step; two of them alternate so that a step's loads have two steps
+  // of compute to arrive (issued at step s - 1, stored to LDS at the end of step s).
+  struct Stage {
+    u32x4 v[NL];
+    float stat, stat2;  // lse, delta
+    int q0;             // first row of slot 0
+  };
+  Stage sa, sb;
+  // fetch side: the step (fh, fp) being loaded and the descriptors of head fh
+  int fh = 0, fp = 0;
+  rsrc_t rq, rd, rl, rt;
+  auto set_head = [&]() {
+    rq = make_rsrc(qslice + int64_t(fh) * 2 * a.sq[1], nq);
+    rd = make_rsrc(dslice + int64_t(fh) * 2 * a.sdo[1], nd);
+    rl = make_rsrc(lslice + int64_t(fh) * 4 * a.slse[1], nl);
+    rt = make_rsrc(tslice + int64_t(fh) * 4 * a.Lp, nt);
+  };
+  // loads the step (fh, fp) into st and moves the fetch side to the next step
+  auto gload = [&](Stage& st) {
+    const uint32_t qb0 = uint32_t(qb_lo + 2 * fp);  // block of slot 0
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int t = i / ITPT, j = i % ITPT;  // compile-time
+      const uint32_t blk = qb0 + uint32_t(t >> 1);
+      if (ALL_ON || lane_on[j])
+        st.v[i] = (t & 1) ? buf_ld16(rd, lane_off_d[j] + blk * bd) : buf_ld16(rq, lane_off_q[j] + blk * bq);
+    }
+    // raw values: any arithmetic on them here would make the wave wait for the loads now
+    const uint32_t blk = qb0 + uint32_t(st_slot);
+    st.stat = buf_ldf(rl, lse_off + blk * bl);
+    st.stat2 = buf_ldf(rt, dlt_off + blk * 128u);
+    st.q0 = 32 * int(qb0);
+    if (++fp == n_qp) {
+      fp = 0;
+      ++fh;
+      if (fh < G) set_head();
     }
   };
-  auto gload = [&](int step) {
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      u32x4 v = zero16();
-      if constexpr (32 * CPR >= 256) {
-        const int tile = (256 * i) / (32 * CPR);          // compile-time
-        const int slot = tile >> 1, tensor = tile & 1;
-        const int rbase = ((256 * i) / CPR) & 31;          // compile-time
-        const int it = 2 * step + slot;
-        const int qr = 32 * (qb_lo + f_qb[slot]) + rbase;  // uniform
-        if (it < n_it && qr + ld_row < L) {
-          const int h = kvh * G + f_h[slot];
-          const int64_t uoff = tensor ? int64_t(h) * a.sdo[1] + int64_t(qr) * a.sdo[2]
-                                      : int64_t(h) * a.sq[1] + int64_t(qr) * a.sq[2];
-          v = ld16((tensor ? dbase : qbase) + 2 * (uoff + (tensor ? dlane : qlane)));
-        }
-      } else {
-        const int c = tid + 256 * i;
-        const int slot = c / (2 * 32 * CPR), tensor = (c / (32 * CPR)) & 1;
-        const int row = (c / CPR) & 31;
-        const int it = 2 * step + slot;
-        const int qrow = 32 * (qb_lo + f_qb[slot]) + row;
-        if (c < NCH && it < n_it && qrow < L) {
-          const int h = kvh * G + f_h[slot];
-          const int64_t off = tensor ? int64_t(h) * a.sdo[1] + int64_t(qrow) * a.sdo[2]
-                                     : int64_t(h) * a.sq[1] + int64_t(qrow) * a.sq[2];
-          v = ld16((tensor ? dbase : qbase) + 2 * off);
-        }
-      }
-      stg[i] = v;
-    }
-    if (tid < 128) {
-      const int slot = tid >> 6, kind = (tid >> 5) & 1, row = tid & 31;
-      const int it = 2 * step + slot;
-      const int qrow = 32 * (qb_lo + f_qb[slot]) + row;
-      stat = kind ? 0.f : __builtin_inff();
-      // raw values: scaling here would make the wave wait for this load (and every load issued
-      // before it) now instead of after the compute of the current step
-      if (it < n_it && qrow < L) {
-        const int h = kvh * G + f_h[slot];
-        stat = kind ? dltbase[int64_t(h) * a.Lp + qrow] : lsebase[int64_t(h) * a.slse[1] + int64_t(qrow) * a.slse[2]];
-      }
-    }
-  };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](const Stage& st, int buf) {
     uint16_t* stage = lds + buf * STAGE;
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int c = tid + 256 * i;
-      if (c < NCH) {
-        const int slot = c / (2 * 32 * CPR), tensor = (c / (32 * CPR)) & 1;
-        const int row = (c / CPR) & 31;
-        st16(stage + slot * SLOT + tensor * TILE + row * ROW + 8 * ld_col, stg[i]);
-      }
+    for (int i = 0; i < NL; ++i) {
+      const int t = i / ITPT, j = i % ITPT;
+      if (ALL_ON || lane_on[j]) st16(stage + (t >> 1) * SLOT + (t & 1) * TILE + lane_lds[j], st.v[i]);
     }
+    // lse -> lse * log2(e) (+inf for rows past L, which read 0: their P is exactly 0);
+    // delta -> -delta, the initial value of the dP accumulator
     if (tid < 128) {
-      const int slot = tid >> 6, kind = (tid >> 5) & 1, row = tid & 31;
-      reinterpret_cast<float*>(stage + slot * SLOT + 2 * TILE)[kind * 32 + row] = kind ? stat : stat * kLog2e;
+      const int qrow = st.q0 + 32 * st_slot + st_row;
+      const float v = st_kind ? -st.stat2 : (qrow < L ? st.stat * kLog2e : __builtin_inff());
+      reinterpret_cast<float*>(stage + st_slot * SLOT + 2 * TILE)[st_kind * 32 + st_row] = v;
     }
   };
 
-  // Per-lane constants of the compute: LDS offsets and the mask threshold.  A key k < S is
-  // visible to every row q >= k (threshold 2^31 on the unsigned q - k); other keys to
-  // 0 <= q - k < W.
+  // Per-lane constants of the compute.  The mask is one unsigned compare per element:
+  //   regular workgroup: q - k < lim, lim = W for ordinary keys, 2^31 for sink keys (any
+  //     q >= k), wqhi - k for sink keys of a block whose later rows belong to chunk workgroups;
+  //   chunk workgroup: q - qlo < lim, lim = qhi - qlo for sink keys, 0 for the others.
   const int a_off = r32 * ROW + hf * (D / 2);
-  const unsigned thr = key < S ? 0x80000000u : unsigned(W);
-  // iteration counters of the item this wave computes
-  int c_h = hh < n_qb ? 0 : 1, c_qb = hh < n_qb ? hh : hh - n_qb;
-  if (n_qb == 0) c_qb = 0;
+  unsigned lim;
+  if (is_chunk) lim = key < S ? unsigned(qhi - qlo) : 0u;
+  else lim = key < S ? (partial_block ? unsigned(max(wqhi - key, 0)) : 0x80000000u) : unsigned(W);
+  const int mref = is_chunk ? qlo : key;  // mask coordinate: row - mref
 
-  if (n_steps > 0) {
-    gload(0);
-    sstore(0);
-    advance();
-  }
-  // Nothing may be outstanding at the loop head: the compiler's wait counting is conservative
-  // across the back edge and would otherwise wait for the next step's prefetch before the first
-  // MFMA of every step.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int step = 0; step < n_steps; ++step) {
-    const bool more = step + 1 < n_steps;
-    if (more) gload(step + 1);
-    const int it = 2 * step + hh;
-    const int qr0 = 32 * (qb_lo + c_qb);
-    if (wave_on && it < n_it && qr0 + 32 > wqlo && qr0 < wqhi && kv_half_needs(qr0, ks0, L, W, S)) {
-      const uint16_t* Qt = lds + (step & 1) * STAGE + hh * SLOT;
-      const uint16_t* Dt = Qt + TILE;
-      const float* lse2 = reinterpret_cast<const float*>(Qt + 2 * TILE);
-      const float* dlt = lse2 + 32;
-      f32x16 sacc = f32x16{}, dpacc = f32x16{};
+  // One item of this wave: the (head, block) pair cp of step `step`, slot hh.
+  auto compute = [&](int step, int cp) {
+    const int qbi = 2 * cp + hh;
+    const int qr0 = 32 * (qb_lo + qbi);
+    if (!(wave_on && qbi < n_qb && qr0 + 32 > wqlo && qr0 < wqhi && kv_half_needs(qr0, ks0, L, W, S))) return;
+    const uint16_t* Qt = lds + (step & 1) * STAGE + hh * SLOT;
+    const uint16_t* Dt = Qt + TILE;
+    const float* lse2 = reinterpret_cast<const float*>(Qt + 2 * TILE);
+    const float* ndlt = lse2 + 32;  // -delta
+    f32x16 sacc = f32x16{}, dpacc;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        sacc = E::mfma(lds16(Qt + a_off + 8 * ks), kf[ks], sacc);
-        dpacc = E::mfma(lds16(Dt + a_off + 8 * ks), vf[ks], dpacc);
-      }
-      const bool inside = qr0 >= wqlo && qr0 + 32 <= wqhi;
-      const bool full = inside && tile_full(ks0, qr0, W, S);
-      const int d0 = qr0 + 4 * hf - key;         // row - key of register e = 0
-      const int r0 = qr0 + 4 * hf - wqlo;        // row - wqlo of register e = 0
-      const unsigned span = unsigned(wqhi - wqlo);
-      float p[16], ds[16];
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(ndlt + 8 * j + 4 * hf);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dpacc[4 * j + i] = d4[i];
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      sacc = E::mfma(lds16(Qt + a_off + 8 * ks), kf[ks], sacc);
+      dpacc = E::mfma(lds16(Dt + a_off + 8 * ks), vf[ks], dpacc);  // dP - delta
+    }
+    const bool full = !is_chunk && qr0 >= wqlo && qr0 + 32 <= wqhi && tile_full(ks0, qr0, W, S);
+    const int m0 = qr0 + 4 * hf - mref;  // mask coordinate of register e = 0
+    float p[16], ds[16];
+    // P = exp2(s*c - lse2) and dS = P (dP - delta); MASK selects the masked variant
+    auto elementwise = [&](auto mask_tag) {
+      constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2 + 8 * j + 4 * hf);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlt + 8 * j + 4 * hf);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int e = 4 * j + i, off = 8 * j + i;
+          const int e = 4 * j + i;
           float pe = fast_exp2(fmaf(sacc[e], a.c, -l4[i]));
-          if (!full) {
-            bool ok = unsigned(d0 + off) < thr;
-            if (!inside) ok &= unsigned(r0 + off) < span;
-            pe = ok ? pe : 0.f;
-          }
+          if constexpr (MASK) pe = unsigned(m0 + 8 * j + i) < lim ? pe : 0.f;
           p[e] = pe;
-          ds[e] = pe * (dpacc[e] - d4[i]);
+          ds[e] = pe * dpacc[e];
         }
       }
-      const u32x4 pb0 = pack8<E>(p), pb1 = pack8<E>(p + 8);
-      const u32x4 sb0 = pack8<E>(ds), sb1 = pack8<E>(ds + 8);
+    };
+    if (full) elementwise(std::false_type{});
+    else elementwise(std::true_type{});
+    const u32x4 pb0 = pack8<E>(p), pb1 = pack8<E>(p + 8);
+    const u32x4 sb0 = pack8<E>(ds), sb1 = pack8<E>(ds + 8);
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
+    for (int db = 0; db < DB; ++db) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const u32x4 dt = tr_frag<ROW>(Dt, 16 * t, 32 * db, D);
-          const u32x4 qt = tr_frag<ROW>(Qt, 16 * t, 32 * db, D);
-          dv[db] = E::mfma(dt, t ? pb1 : pb0, dv[db]);
-          dk[db] = E::mfma(qt, t ? sb1 : sb0, dk[db]);
-        }
+      for (int t = 0; t < 2; ++t) {
+        const u32x4 dt = tr_frag<ROW>(Dt, 16 * t, 32 * db, D);
+        const u32x4 qt = tr_frag<ROW>(Qt, 16 * t, 32 * db, D);
+        dv[db] = E::mfma(dt, t ? pb1 : pb0, dv[db]);
+        dk[db] = E::mfma(qt, t ? sb1 : sb0, dk[db]);
       }
     }
-    // next item of this wave's slot
-    c_qb += 2;
-    while (c_qb >= n_qb && n_qb > 0) {
-      c_qb -= n_qb;
-      ++c_h;
-    }
-    if (more) {
-      sstore((step + 1) & 1);
-      advance();
-    }
+  };
+
+  // Descriptors are built before any load, whatever the number of steps (a workgroup can own
+  // no items: a chunk whose rows all lie inside the window).
+  set_head();
+  if (n_steps > 0) {
+    gload(sa);
+    sstore(sa, 0);
+    // Nothing may be outstanding here: the compiler's wait counting is conservative across the
+    // loop's back edge and would otherwise wait for in-flight prefetches before every MFMA.
+    __builtin_amdgcn_s_waitcnt(0);
+    gload(sa);  // step 1
+  }
+  __syncthreads();
+  // Step s computes LDS buffer s & 1, issues the loads of step s + 2 and stores step s + 1
+  // (loaded during step s - 1) into the other buffer.
+  // The loads are issued unconditionally (past the last step they read the last head's rows or
+  // zeros and are never used), so the wait counts before the LDS stores are exact.
+  int cp = 0;  // block pair of the step being computed
+  for (int step = 0; step < n_steps; step += 2) {
+    gload(sb);
+    compute(step, cp);
+    if (++cp == n_qp) cp = 0;
+    if (step + 1 < n_steps) sstore(sa, 1);
+    __syncthreads();
+    if (step + 1 >= n_steps) break;
+    gload(sa);
+    compute(step + 1, cp);
+    if (++cp == n_qp) cp = 0;
+    if (step + 2 < n_steps) sstore(sb, 0);
     __syncthreads();
   }
 

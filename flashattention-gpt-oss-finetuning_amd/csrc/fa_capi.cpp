@@ -30,6 +30,12 @@ bool lse_strides_ok(const int64_t s[3]) { return s[0] >= 0 && s[1] >= 0 && s[2] 
 
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
+// The kernels address one (batch, head) slice of a tensor with 32-bit byte offsets: its L rows
+// must span fewer than 2^31 bytes.
+bool slice_fits(const int64_t s[3], int L, int D, int elem_bytes) {
+  return (int64_t(L - 1) * s[2] + D) * elem_bytes < (int64_t(1) << 31);
+}
+
 int check_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t L, int32_t D, int32_t W, int32_t S,
                  float scale, int32_t dtype) {
   if (B < 1 || Hq < 1 || Hkv < 1 || L < 1) return FA_ERR_SHAPE;
@@ -151,6 +157,9 @@ int fa_check_bwd(const fa_bwd_params* p) {
       !strides_ok(p->o_stride) || !strides_ok(p->do_stride) || !lse_strides_ok(p->lse_stride) ||
       !strides_ok(p->dq_stride) || !strides_ok(p->dk_stride) || !strides_ok(p->dv_stride))
     return FA_ERR_ALIGN;
+  const int L = p->seqlen, D = p->head_dim;
+  if (!slice_fits(p->q_stride, L, D, 2) || !slice_fits(p->do_stride, L, D, 2) || !slice_fits(p->lse_stride, L, 1, 4))
+    return FA_ERR_OVERFLOW;
   return FA_OK;
 }
 

@@ -109,6 +109,24 @@ __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4
 __device__ __forceinline__ u32x4 zero16() { return u32x4{0u, 0u, 0u, 0u}; }
 __device__ __forceinline__ u32x4 lds16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+// Buffer resources: a scalar descriptor of [base, base + bytes); vector loads at byte offsets
+// >= bytes return zeros, so tile edges need no branches.  (0x00020000: 32-bit data format of
+// the gfx9 descriptor word 3.)
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_ld16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float buf_ldf(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+// Bytes spanned by `rows` rows of `cols` 16-bit elements with row stride `stride` (0 if none).
+__device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride, int cols) {
+  return rows > 0 ? uint32_t((int64_t(rows - 1) * stride + cols) * 2) : 0u;
+}
+
 // ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, output lane i, element j is
 // element (i & 3) of the 8 bytes addressed by lane 4j + (i >> 2) of the group.  (Checked on
 // hardware by an in-bounds probe.)  Reading 4 rows x 16 columns of a row-major LDS tile this way

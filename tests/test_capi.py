@@ -155,6 +155,19 @@ def test_check_bwd_codes(over, code):
     assert _lib.lib().fa_check_bwd(ctypes.byref(_bwd_params(**over))) == code
 
 
+def test_check_bwd_rejects_slices_beyond_32bit_offsets():
+    """The backward kernels address one (batch, head) slice of q/dout/lse with 32-bit byte
+    offsets; a slice spanning 2^31 bytes or more is refused instead of wrapping."""
+    L = _lib.lib()
+    big = 1 << 20  # rows
+    ok = _bwd_params(seqlen=big, q_stride=(64 * big * 64, big * 64, 64), do_stride=(64 * big * 64, big * 64, 64),
+                     dq_stride=(64 * big * 64, big * 64, 64), lse_stride=(8 * big, big, 1))
+    assert L.fa_check_bwd(ctypes.byref(ok)) == _lib.FA_OK  # (2^20 - 1) * 64 + 64 elements * 2 B < 2^31
+    wide = _bwd_params(seqlen=big, q_stride=(8 * big * 1024, 1024, 8 * 1024), do_stride=(64 * big * 64, big * 64, 64),
+                       dq_stride=(64 * big * 64, big * 64, 64), lse_stride=(8 * big, big, 1))
+    assert L.fa_check_bwd(ctypes.byref(wide)) == _lib.FA_ERR_OVERFLOW
+
+
 def test_entry_points_reject_before_any_hip_call():
     """fa_fwd / fa_bwd return the validation code for bad arguments (this runs without a GPU)."""
     L = _lib.lib()
