@@ -25,8 +25,6 @@ struct Args {
   // backward workspace
   float* delta;      // [B][Hq][Lp] fp32, Lp = L rounded up to 32
   float* partial;    // sink-key partial sums, see fa_bwd.hip
-  unsigned* counters;  // per sink block arrival counters of the dK/dV kernel
-  int n_counters;
   int64_t sq[3], sk[3], sv[3], so[3], sdo[3], slse[3], sdq[3], sdk[3], sdv[3], so_out[3];
   int B, Hq, Hkv, L, G, Lp;
   int W, S;          // window and sink, clamped to [0, L]
@@ -44,7 +42,7 @@ struct Args {
   int n_chunk_wgs;   // B * Hkv * nsp * n_chunks
 };
 
-// Launchers (return the hipError_t of the launch).
+// Launchers (return the hipError_t of the launch; launch_bwd_dkdv also launches the sink fold).
 hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
 hipError_t launch_bwd_dq(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
 hipError_t launch_bwd_dkdv(const Args& a, int dtype, int D, hipStream_t stream);

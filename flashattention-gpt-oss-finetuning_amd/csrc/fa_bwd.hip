@@ -8,7 +8,7 @@
 //     dQ = scale * dS K,  dK = scale * dS^T Q,  dV = P^T dO,
 // dK/dV summed over the query heads that share a KV head.
 //
-// Two launches:
+// Launches:
 //  1. bwd_dq_kernel (query-major, same tiling as the forward): computes delta for its rows
 //     (stored in the workspace) and dQ over the sink + window key blocks.
 //  2. bwd_dkdv_kernel (key-major): a workgroup owns 64 keys of one KV head and sweeps the
@@ -18,6 +18,7 @@
 //     chunks of `chunk_rows` handled by extra workgroups of the same kernel (the reference
 //     instead loops one program over all of L for a sink block,
 //     benchmark_backward_speed.py:432-438).
+//  3. bwd_sink_fold_kernel (only when rows were chunked): adds the sink rows' partial sums.
 #include <type_traits>
 
 #include "fa_args.h"
@@ -93,10 +94,6 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
       if (hf == 0) a.delta[(int64_t(b) * a.Hq + hw + h) * a.Lp + q] = delta[h];
     }
   }
-
-  // The dK/dV kernel's per-block arrival counters start at zero.
-  if (tile == 0)
-    for (int i = tid; i < a.n_counters; i += 256) a.counters[i] = 0u;
 
   f32x16 acc[HPW][DB];
 #pragma unroll
@@ -258,8 +255,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
 //
 // Sink keys: for the first `nsp` blocks the rows past the window are handled by chunk
 // workgroups; every workgroup of such a block writes the fp32 partial sums of its sink rows to
-// the workspace, and the last one to arrive (a counter per block, zeroed by the dQ kernel and
-// reset by its last user) adds them in a fixed order and writes those rows.
+// its own slot of the workspace, and bwd_sink_fold_kernel adds the slots in a fixed order.
 // ---------------------------------------------------------------------------------------------
 template <typename E, int D>
 __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
@@ -270,12 +266,9 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   constexpr int SLOT = 2 * TILE + 128;       // Q, dO, then lse2[32] and delta[32] as fp32
   constexpr int STAGE = 2 * SLOT;            // two items per step
   constexpr int CPR = D / 8;                 // 16-byte chunks per row
-  constexpr int NCH = 2 * 2 * 32 * CPR;      // chunks per step
-  constexpr int NLD = (NCH + 255) / 256;     // chunks per thread
   constexpr int RED = 2 * 2 * DB * 16 * 64;  // fp32 partials of the two hh = 1 waves
   constexpr int LDS_ELEMS = (2 * STAGE > 2 * RED) ? 2 * STAGE : 2 * RED;
   __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];
-  __shared__ int last_flag;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -590,31 +583,38 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
       }
     }
   }
-  if (!partial_block) return;
+}
 
-  // ---- last workgroup of a sink block: fixed-order sum of the n_chunks + 1 partials -----------
-  __threadfence();
-  __syncthreads();
-  const int64_t blk = (int64_t(b) * a.Hkv + kvh) * a.nsp + kblk;
-  if (tid == 0) last_flag = atomicAdd(&a.counters[blk], 1u) == unsigned(a.n_chunks);
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-  const int nrows = min(kKvKeys, min(S, L) - kKvKeys * kblk);
-  const float* base = a.partial + blk * (a.n_chunks + 1) * 2 * kKvKeys * D;
-  for (int i = tid; i < 2 * nrows * D; i += 256) {
-    const int part = i / (nrows * D), rem = i % (nrows * D);
-    const int row = rem / D, d = rem % D;
-    const float* src = base + part * kKvKeys * D + row * D + d;
-    float sum = 0.f;
-    for (int sl = 0; sl <= a.n_chunks; ++sl) sum += src[int64_t(sl) * 2 * kKvKeys * D];
-    const int k2 = kKvKeys * kblk + row;
-    uint16_t* dst = reinterpret_cast<uint16_t*>(part ? a.dv : a.dk) +
-                    int64_t(b) * (part ? a.sdv[0] : a.sdk[0]) + int64_t(kvh) * (part ? a.sdv[1] : a.sdk[1]) +
-                    int64_t(k2) * (part ? a.sdv[2] : a.sdk[2]) + d;
-    *dst = uint16_t(E::pack2(part ? sum : sum * a.scale, 0.f));
+// ---------------------------------------------------------------------------------------------
+// Sink fold: the dK/dV rows of the chunked sink keys are the sum, in slot order, of the fp32
+// partials that the dK/dV kernel's regular and chunk workgroups wrote for them.  A separate
+// launch, so the partials of every workgroup are visible without a device-wide fence inside the
+// dK/dV kernel.  One thread per (b, KV head, sink key, head-dim index); only keys < S of the
+// chunked blocks exist here.
+// ---------------------------------------------------------------------------------------------
+template <typename E, int D>
+__global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
+  const int nrows = min(a.S, kKvKeys * a.nsp);  // sink keys of the chunked blocks
+  const int64_t n = int64_t(a.B) * a.Hkv * nrows * D;
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int d = int(i % D);
+  const int key = int((i / D) % nrows);
+  const int64_t bh = i / (int64_t(nrows) * D);  // b * Hkv + kvh
+  const int kvh = int(bh % a.Hkv), b = int(bh / a.Hkv);
+  const int kblk = key / kKvKeys, row = key % kKvKeys;
+  const int64_t blk = bh * a.nsp + kblk;
+  const float* src = a.partial + blk * (a.n_chunks + 1) * 2 * kKvKeys * D + row * D + d;
+  float sk = 0.f, sv = 0.f;
+  for (int sl = 0; sl <= a.n_chunks; ++sl) {
+    sk += src[int64_t(sl) * 2 * kKvKeys * D];
+    sv += src[int64_t(sl) * 2 * kKvKeys * D + kKvKeys * D];
   }
-  if (tid == 0) a.counters[blk] = 0u;
+  const uint32_t pk = E::pack2(sk * a.scale, sv);
+  reinterpret_cast<uint16_t*>(a.dk)[int64_t(b) * a.sdk[0] + int64_t(kvh) * a.sdk[1] + int64_t(key) * a.sdk[2] + d] =
+      uint16_t(pk);
+  reinterpret_cast<uint16_t*>(a.dv)[int64_t(b) * a.sdv[0] + int64_t(kvh) * a.sdv[1] + int64_t(key) * a.sdv[2] + d] =
+      uint16_t(pk >> 16);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -631,6 +631,10 @@ template <typename E, int D>
 static hipError_t launch_dkdv_d(const Args& a, hipStream_t stream) {
   const dim3 grid(a.n_chunk_wgs + a.B * a.Hkv * a.n_kblocks), block(256);
   hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), grid, block, 0, stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.nsp == 0) return e;
+  const int64_t n = int64_t(a.B) * a.Hkv * min(a.S, kKvKeys * a.nsp) * D;
+  hipLaunchKernelGGL((bwd_sink_fold_kernel<E, D>), dim3(unsigned((n + 255) / 256)), block, 0, stream, a);
   return hipGetLastError();
 }
 

@@ -93,10 +93,6 @@ size_t partial_bytes(int B, int Hkv, int D, const SinkPlan& sp) {
   return align256(size_t(B) * Hkv * sp.nsp * (sp.n_chunks + 1) * 2 * fa::kKvKeys * D * sizeof(float));
 }
 
-size_t counter_bytes(int B, int Hkv, const SinkPlan& sp) {
-  return align256(size_t(B) * Hkv * sp.nsp * sizeof(unsigned));
-}
-
 void copy3(int64_t dst[3], const int64_t src[3]) {
   for (int i = 0; i < 3; ++i) dst[i] = src[i];
 }
@@ -192,8 +188,7 @@ size_t fa_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t heads_kv, 
   if (check_common(batch, heads_q, heads_kv, seqlen, head_dim, window, sink, 1.f, FA_DTYPE_BF16) != FA_OK)
     return 0;
   const SinkPlan sp = sink_plan(seqlen, window, sink);
-  return delta_bytes(batch, heads_q, seqlen) + partial_bytes(batch, heads_kv, head_dim, sp) +
-         counter_bytes(batch, heads_kv, sp);
+  return delta_bytes(batch, heads_q, seqlen) + partial_bytes(batch, heads_kv, head_dim, sp);
 }
 
 }  // extern "C"
@@ -239,8 +234,6 @@ int prepare_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
   const SinkPlan sp = sink_plan(a.L, p->window, p->sink);
   char* ws = static_cast<char*>(workspace);
   a.partial = reinterpret_cast<float*>(ws + delta_bytes(a.B, a.Hq, a.L));
-  a.counters = reinterpret_cast<unsigned*>(ws + delta_bytes(a.B, a.Hq, a.L) + partial_bytes(a.B, a.Hkv, p->head_dim, sp));
-  a.n_counters = a.B * a.Hkv * sp.nsp;
   a.n_kblocks = (a.L + fa::kKvKeys - 1) / fa::kKvKeys;
   a.nsp = sp.nsp;
   a.n_chunks = sp.n_chunks;

@@ -189,12 +189,11 @@ def test_workspace_bytes():
     assert ws(1, 8, 2, 128, 64, 200, 4) == 8 * 128 * 4
     assert ws(1, 8, 2, 100, 64, 200, 4) == 8 * 128 * 4
     # sink split: 1 block of 64 keys, ceil(L/256) chunks + the regular slot, dK and dV,
-    # 64 rows x D fp32 each, then one 4-byte arrival counter per (batch, KV head, block)
+    # 64 rows x D fp32 each
     L_, D = 4096, 64
     expect_delta = 64 * 4096 * 4
     expect_partial = 8 * 1 * (16 + 1) * 2 * 64 * D * 4
-    expect_counters = 256  # 8 counters, 256-byte aligned
-    assert ws(1, 64, 8, L_, D, 128, 4) == expect_delta + expect_partial + expect_counters
+    assert ws(1, 64, 8, L_, D, 128, 4) == expect_delta + expect_partial
     # invalid problems give 0
     assert ws(1, 8, 3, 128, 64, 16, 4) == 0
     assert ws(1, 8, 2, 128, 64, 0, 0) == 0
