@@ -13,7 +13,9 @@ same way.  Prints ONE JSON line.
                (14*D FLOPs per pair per head), whole job
   ms_per_step  fwd+bwd milliseconds
   roofline     the dominant kernel: algorithmic bytes (or FLOPs) per launch / its average
-               duration measured with HIP events on the launch stream
+               duration measured with HIP events on the launch stream; `traffic` is its HBM
+               bytes per launch from the copy-calibrated rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+               in profiles/<config>_hbm_traffic.txt (null without one)
   cpu_baseline the reference's naive PyTorch path (oracle/naive.py, in the config dtype) timed
                on the host cores on a bounded sample (whole KV groups of the same workload)
 """
@@ -48,6 +50,7 @@ CONFIGS = {
 }
 
 HBM_PEAK_GBS = 8000.0
+COPY_BYTES = 256 << 20
 MFMA_PEAK_TFLOPS = 2500.0
 
 
@@ -91,6 +94,29 @@ def kernel_accounting(cfg):
     }
 
 
+# Kernels launched by each stage of the C ABI (fa_bwd_dkdv also launches the sink fold).
+STAGE_KERNELS = {"fwd": ["fwd_kernel"], "bwd_dq": ["bwd_dq_kernel"],
+                 "bwd_dkdv": ["bwd_dkdv_kernel", "bwd_sink_fold_kernel"]}
+
+
+def measured_traffic(config, stage):
+    """HBM bytes per launch of a stage, from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed
+    as profiles/<config>_hbm_traffic.txt (copy-calibrated); None when there is no summary."""
+    path = os.path.join(ROOT, "profiles", f"{config}_hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    rows = {}
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) == 4 and parts[0].endswith("_kernel") and parts[3].isdigit():
+                rows[parts[0]] = int(parts[3])
+    names = STAGE_KERNELS[stage]
+    if names[0] not in rows:
+        return None
+    return float(sum(rows.get(n, 0) for n in names))
+
+
 def time_kernels(cfg, q, k, v, do, iters=50):
     """Average duration of each kernel, launched alone through the C ABI, measured with HIP events
     recorded on the stream the kernel is launched on (torch's current stream)."""
@@ -118,6 +144,29 @@ def time_kernels(cfg, q, k, v, do, iters=50):
         torch.cuda.synchronize()
         out[name] = t0.elapsed_time(t1) / iters * 1e3  # microseconds
     return out
+
+
+def profile_launches(cfg, q, k, v, do, n):
+    """A short program for hardware-counter runs: n launches of a plain 256 MiB device copy (the
+    calibration for FETCH_SIZE / WRITE_SIZE: it reads and writes exactly 256 MiB), then n launches
+    of each kernel of the path, with a synchronization between the groups."""
+    import torch
+
+    ops = _mod("_ops")
+    scale = 1.0 / math.sqrt(cfg["D"])
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=q.device).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(n):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    fc = ops.FwdCall(q, k, v, cfg["W"], cfg["S"], scale)
+    bc = ops.BwdCall(q, k, v, fc.o, fc.lse, do, cfg["W"], cfg["S"], scale)
+    for fn in (fc.run, lambda: bc.run("dq"), lambda: bc.run("dkdv")):
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+    print(f"profile_launches: {n} x copy {COPY_BYTES} B, fwd, bwd_dq, bwd_dkdv on {cfg['name']}", flush=True)
 
 
 def time_steps(fa, cfg, q, k, v, do, steps, warmup):
@@ -236,6 +285,8 @@ def main():
     ap.add_argument("--cpu-baseline-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--table", action="store_true", help="also time every BASELINE config (stderr)")
+    ap.add_argument("--profile-launches", type=int, default=0, metavar="N",
+                    help="only launch a 256 MiB copy and each kernel N times (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -254,6 +305,9 @@ def main():
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda", 0)
     q, k, v, do = make_inputs(cfg, dev)
+    if args.profile_launches:
+        profile_launches(cfg, q, k, v, do, args.profile_launches)
+        return
     acct = kernel_accounting(cfg)
     wl = _mod("flops").Workload(cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"], cfg["D"], cfg["W"], cfg["S"])
 
@@ -274,7 +328,8 @@ def main():
     else:
         achieved, peak, unit = dk["tflops"], MFMA_PEAK_TFLOPS, "TFLOP/s"
     roofline = {"kernel": dom, "bound": dk["bound"], "achieved": achieved, "peak": peak, "unit": unit,
-                "frac": round(achieved / peak, 4), "traffic": None, "avg_us": dk["avg_us"]}
+                "frac": round(achieved / peak, 4), "traffic": measured_traffic(args.config, dom),
+                "avg_us": dk["avg_us"], "alg_bytes": dk["alg_bytes"]}
 
     fb_flops = wl.flops("fwdbwd")
     value = fb_flops / (t["fwdbwd_ms"] * 1e-3) / 1e12

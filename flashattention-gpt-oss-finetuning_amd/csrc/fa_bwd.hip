@@ -605,10 +605,25 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
   const int kblk = key / kKvKeys, row = key % kKvKeys;
   const int64_t blk = bh * a.nsp + kblk;
   const float* src = a.partial + blk * (a.n_chunks + 1) * 2 * kKvKeys * D + row * D + d;
+  // Slots are added in order; the loads of up to kBatch slots are in flight together.
+  constexpr int kBatch = 16;
+  constexpr int64_t kSlot = 2 * kKvKeys * D;
+  const int ns = a.n_chunks + 1;
   float sk = 0.f, sv = 0.f;
-  for (int sl = 0; sl <= a.n_chunks; ++sl) {
-    sk += src[int64_t(sl) * 2 * kKvKeys * D];
-    sv += src[int64_t(sl) * 2 * kKvKeys * D + kKvKeys * D];
+  for (int s0 = 0; s0 < ns; s0 += kBatch) {
+    float xk[kBatch], xv[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const bool in = s0 + j < ns;
+      const float* p = src + int64_t(in ? s0 + j : 0) * kSlot;
+      xk[j] = in ? p[0] : 0.f;
+      xv[j] = in ? p[kKvKeys * D] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      sk += xk[j];
+      sv += xv[j];
+    }
   }
   const uint32_t pk = E::pack2(sk * a.scale, sv);
   reinterpret_cast<uint16_t*>(a.dk)[int64_t(b) * a.sdk[0] + int64_t(kvh) * a.sdk[1] + int64_t(key) * a.sdk[2] + d] =
