@@ -53,6 +53,11 @@ struct BF16 {
   static __device__ __forceinline__ float to_f32(uint16_t bits) {
     return __builtin_bit_cast(float, uint32_t(bits) << 16);
   }
+  // acc + lo + hi of a packed pair (v_dot2 with ones)
+  static __device__ __forceinline__ float sum2(uint32_t pair, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
+                                           __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
+  }
 };
 
 struct F16 {
@@ -66,6 +71,10 @@ struct F16 {
   }
   static __device__ __forceinline__ float to_f32(uint16_t bits) {
     return float(__builtin_bit_cast(_Float16, bits));
+  }
+  static __device__ __forceinline__ float sum2(uint32_t pair, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), __builtin_bit_cast(f16x2, 0x3c003c00u), acc,
+                                  false);
   }
 };
 
@@ -160,6 +169,32 @@ __device__ __forceinline__ float xor32(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
                                        int((threadIdx.x ^ 32) & 63) << 2, __builtin_bit_cast(int, x)));
 }
+
+// v_permlane32_swap v_a, v_b swaps the upper 32 lanes of v_a with the lower 32 lanes of v_b.
+// Given the same value x in both, v_a ends up holding x of lane (l & 31) and v_b x of lane
+// (l & 31) + 32, on every lane (checked on hardware), so max/sum of the two wave halves need no
+// LDS round trip and both halves get bitwise the same result.  Written as inline asm: the
+// builtin's second result is miscompiled at -O3 by the ROCm 7.2 compiler (folded into the
+// first).  The s_nop covers the VALU-write -> permlane-read hazard of the operands.
+__device__ __forceinline__ void halves(float x, float& lo, float& hi) {
+  uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  lo = __builtin_bit_cast(float, a);
+  hi = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float max_halves(float x) {
+  float lo, hi;
+  halves(x, lo, hi);
+  return fmaxf(lo, hi);
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  float lo, hi;
+  halves(x, lo, hi);
+  return lo + hi;
+}
+
+// True on every lane when the predicate holds on any active lane (wave-uniform branch).
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }

@@ -21,6 +21,8 @@
 
 namespace fa {
 
+constexpr float kRescaleGap = 8.f;  // log2 units: P stays <= 256 between rescales
+
 template <typename E, int D, int HPW>
 __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   constexpr int BN = 64;                   // keys per LDS block
@@ -142,51 +144,66 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
       for (int sb = 0; sb < 2; ++sb) {
         const int ks0 = kb + 32 * sb;
         if (!wave_needs(ks0, qw, L, W, S)) continue;
+        // Mask as an additive bias: S^T starts from 0 (allowed) or -inf (masked) in the
+        // accumulator of its first MFMA, shared by the heads of the wave.  Register e of this
+        // lane holds key ks0 + 4hf + off(e), off(e) = 8(e/4) + e%4, of row q; with
+        // dq0 = q - ks0 - 4hf the test is one unsigned compare, allowed = (dq0 - off) < lim with
+        // lim = W for ordinary keys and 2^31 for sink keys (any q >= k).  Which form applies is
+        // wave-uniform.
+        f32x16 bias = f32x16{};
+        if (!tile_full(ks0, qw, W, S)) {
+          const int dq0 = q - ks0 - 4 * hf;
+          if (ks0 >= S || ks0 + 32 <= S) {  // one limit for all 32 keys
+            const unsigned lim = ks0 >= S ? unsigned(W) : 0x80000000u;
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              bias[e] = unsigned(dq0 - (8 * (e / 4) + (e % 4))) < lim ? 0.f : kNegInf;
+          } else {  // the sink boundary S falls inside these keys
+            const int sl = S - ks0 - 4 * hf;  // keys with off < sl are sinks
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int off = 8 * (e / 4) + (e % 4);
+              bias[e] = unsigned(dq0 - off) < (off < sl ? 0x80000000u : unsigned(W)) ? 0.f : kNegInf;
+            }
+          }
+        }
         // S^T = K Q^T for every head of the wave (the K fragment is shared).
         f32x16 s[HPW];
-#pragma unroll
-        for (int h = 0; h < HPW; ++h) s[h] = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           const u32x4 kf = *reinterpret_cast<const u32x4*>(Kl + (32 * sb + r32) * KROW + hf * (D / 2) + 8 * ks);
 #pragma unroll
-          for (int h = 0; h < HPW; ++h) s[h] = E::mfma(kf, qf[h][ks], s[h]);
+          for (int h = 0; h < HPW; ++h) s[h] = E::mfma(kf, qf[h][ks], ks == 0 ? bias : s[h]);
         }
-        const bool full = tile_full(ks0, qw, W, S);
         u32x4 pb[HPW][2];
 #pragma unroll
         for (int h = 0; h < HPW; ++h) {
+          float mx = s[h][0];
+#pragma unroll
+          for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s[h][e]);
+          mx = max_halves(mx) * a.c;  // row max in the log2 domain (-inf stays -inf)
+          // Lazy rescaling: the exponent reference m2 moves only when some row's maximum exceeds
+          // it by more than kRescaleGap, so P <= 2^kRescaleGap and the rescale of the
+          // accumulators is skipped on most steps.  Results are the same up to rounding.
+          if (wave_any(mx > m2[h] + kRescaleGap)) {
+            const float mnew = fmaxf(m2[h], mx);
+            const float alpha = mnew == kNegInf ? 1.f : fast_exp2(m2[h] - mnew);
+            m2[h] = mnew;
+            lsum[h] *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) acc[h][db] *= alpha;
+          }
+          const float ms = m2[h] == kNegInf ? 0.f : m2[h];
           float sv[16];
 #pragma unroll
-          for (int e = 0; e < 16; ++e) sv[e] = s[h][e];
-          if (!full) {
-            const int kl = ks0 + 4 * hf;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              const int off = 8 * (e / 4) + (e % 4);
-              sv[e] = allowed(q - kl - off, kl + off, W, S) ? sv[e] : kNegInf;
-            }
-          }
-          float mx = sv[0];
-#pragma unroll
-          for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sv[e]);
-          mx = fmaxf(mx, xor32(mx));
-          const float mxs = mx == kNegInf ? kNegInf : mx * a.c;
-          const float mnew = fmaxf(m2[h], mxs);
-          const float alpha = mnew == kNegInf ? 1.f : fast_exp2(m2[h] - mnew);
-          const float ms = mnew == kNegInf ? 0.f : mnew;
-          float ps = 0.f;
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            sv[e] = fast_exp2(fmaf(sv[e], a.c, -ms));
-            ps += sv[e];
-          }
-          lsum[h] = lsum[h] * alpha + ps;
-          m2[h] = mnew;
-#pragma unroll
-          for (int db = 0; db < DB; ++db) acc[h][db] *= alpha;
+          for (int e = 0; e < 16; ++e) sv[e] = fast_exp2(fmaf(s[h][e], a.c, -ms));
           pb[h][0] = pack8<E>(sv);
           pb[h][1] = pack8<E>(sv + 8);
+          // the row sum adds the 16-bit P that the PV product uses
+#pragma unroll
+          for (int w = 0; w < 4; ++w) lsum[h] = E::sum2(pb[h][0][w], lsum[h]);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) lsum[h] = E::sum2(pb[h][1][w], lsum[h]);
         }
         // O^T += V^T P^T (the V^T fragment is shared by the heads).
         const int vrow = sigma32(r32);
@@ -210,7 +227,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   if (!wave_active) return;
 #pragma unroll
   for (int h = 0; h < HPW; ++h) {
-    const float lt = lsum[h] + xor32(lsum[h]);
+    const float lt = sum_halves(lsum[h]);
     if (q >= L) continue;
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     char* op = reinterpret_cast<char*>(a.o_out) +
