@@ -135,6 +135,8 @@ int fa_check_fwd(const fa_fwd_params* p) {
   if (!strides_ok(p->q_stride) || !strides_ok(p->k_stride) || !strides_ok(p->v_stride) ||
       !strides_ok(p->o_stride) || !lse_strides_ok(p->lse_stride))
     return FA_ERR_ALIGN;
+  const int L = p->seqlen, D = p->head_dim;
+  if (!slice_fits(p->k_stride, L, D, 2) || !slice_fits(p->v_stride, L, D, 2)) return FA_ERR_OVERFLOW;
   return FA_OK;
 }
 
@@ -154,7 +156,8 @@ int fa_check_bwd(const fa_bwd_params* p) {
       !strides_ok(p->dq_stride) || !strides_ok(p->dk_stride) || !strides_ok(p->dv_stride))
     return FA_ERR_ALIGN;
   const int L = p->seqlen, D = p->head_dim;
-  if (!slice_fits(p->q_stride, L, D, 2) || !slice_fits(p->do_stride, L, D, 2) || !slice_fits(p->lse_stride, L, 1, 4))
+  if (!slice_fits(p->q_stride, L, D, 2) || !slice_fits(p->do_stride, L, D, 2) || !slice_fits(p->lse_stride, L, 1, 4) ||
+      !slice_fits(p->k_stride, L, D, 2) || !slice_fits(p->v_stride, L, D, 2))
     return FA_ERR_OVERFLOW;
   return FA_OK;
 }

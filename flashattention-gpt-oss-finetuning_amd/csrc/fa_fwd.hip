@@ -28,10 +28,11 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   constexpr int BN = 64;                   // keys per LDS block
   constexpr int KS = D / 16;               // reduction steps over the head dim
   constexpr int DB = D >= 32 ? D / 32 : 1; // 32-row C tiles of O^T
-  constexpr int KROW = D + 8;              // K row stride in LDS (elements)
-  constexpr int VROW = BN + 8;             // V^T row stride in LDS (elements)
-  constexpr int BUF = BN * KROW + D * VROW;
-  constexpr int NK = (BN * D / 8 + 255) / 256;  // 16-byte K chunks per thread
+  constexpr int KROW = D + 8;              // K and V row stride in LDS (elements)
+  constexpr int BUF = 2 * BN * KROW;       // K, then V, both row-major [key][d]
+  constexpr int CPB = BN * D / 8;          // 16-byte chunks per 64-key block of K (or V)
+  constexpr int NK = (CPB + 255) / 256;    // chunks per thread
+  constexpr bool ALL_ON = CPB >= 256;      // every thread loads a chunk of every tile
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF];
 
   const int tid = threadIdx.x;
@@ -82,31 +83,33 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // Key block enumeration for the workgroup's rows [q0, q_end).
   const QPlan plan = qplan(q0, BM, L, W, S);
 
-  const char* kbase = reinterpret_cast<const char*>(a.k) + 2 * (int64_t(b) * a.sk[0] + int64_t(kvh) * a.sk[1]);
-  const char* vbase = reinterpret_cast<const char*>(a.v) + 2 * (int64_t(b) * a.sv[0] + int64_t(kvh) * a.sv[1]);
+  // K/V of the KV head through buffer resources spanning rows [0, L): rows past L read as zero,
+  // so the loads need no branches (a slice is < 2^31 bytes, checked by the C ABI).
+  const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * (int64_t(b) * a.sk[0] + int64_t(kvh) * a.sk[1]),
+                              span_bytes(L, a.sk[2], D));
+  const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * (int64_t(b) * a.sv[0] + int64_t(kvh) * a.sv[1]),
+                              span_bytes(L, a.sv[2], D));
+  // chunk it of this thread: row c / (D/8), 8 elements from column 8 (c % (D/8)), c = tid + 256 it
+  uint32_t off_k[NK], off_v[NK];
+  int off_l[NK];
+#pragma unroll
+  for (int it = 0; it < NK; ++it) {
+    const int c = tid + 256 * it;
+    const int row = c / (D / 8), col = c % (D / 8);
+    off_k[it] = uint32_t((int64_t(row) * a.sk[2] + 8 * col) * 2);
+    off_v[it] = uint32_t((int64_t(row) * a.sv[2] + 8 * col) * 2);
+    off_l[it] = row * KROW + 8 * col;
+  }
+  const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
 
   // Register staging of the next LDS block.
-  u32x4 kreg[NK];
-  u32x4 vreg[4];
-  const int v_dc = tid % (D / 8), v_kq = tid / (D / 8);  // V unit: 8 head-dim x 4 keys
-  const bool v_loader = tid < 2 * D;
-
+  u32x4 kreg[NK], vreg[NK];
   auto gload = [&](int kb) {
 #pragma unroll
     for (int it = 0; it < NK; ++it) {
-      const int c = tid + 256 * it;
-      const int row = c / (D / 8), col = c % (D / 8);
-      u32x4 v = zero16();
-      if (c < BN * D / 8 && kb + row < L) v = ld16(kbase + 2 * (int64_t(kb + row) * a.sk[2] + 8 * col));
-      kreg[it] = v;
-    }
-    if (v_loader) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kb + 4 * v_kq + r;
-        u32x4 v = zero16();
-        if (key < L) v = ld16(vbase + 2 * (int64_t(key) * a.sv[2] + 8 * v_dc));
-        vreg[r] = v;
+      if (ALL_ON || tid + 256 * it < CPB) {
+        kreg[it] = buf_ld16(rk, off_k[it] + uint32_t(kb) * bk);
+        vreg[it] = buf_ld16(rv, off_v[it] + uint32_t(kb) * bv);
       }
     }
   };
@@ -115,17 +118,10 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     uint16_t* Vl = Kl + BN * KROW;
 #pragma unroll
     for (int it = 0; it < NK; ++it) {
-      const int c = tid + 256 * it;
-      const int row = c / (D / 8), col = c % (D / 8);
-      if (c < BN * D / 8) st16(Kl + row * KROW + 8 * col, kreg[it]);
-    }
-    if (v_loader) {
-      u32x2 cols[8];
-      transpose4x8(vreg, cols);
-      const int pos = perm_pos(4 * v_kq);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        *reinterpret_cast<u32x2*>(Vl + (8 * v_dc + i) * VROW + pos) = cols[i];
+      if (ALL_ON || tid + 256 * it < CPB) {
+        st16(Kl + off_l[it], kreg[it]);
+        st16(Vl + off_l[it], vreg[it]);
+      }
     }
   };
 
@@ -144,14 +140,25 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
       for (int sb = 0; sb < 2; ++sb) {
         const int ks0 = kb + 32 * sb;
         if (!wave_needs(ks0, qw, L, W, S)) continue;
-        // Mask as an additive bias: S^T starts from 0 (allowed) or -inf (masked) in the
-        // accumulator of its first MFMA, shared by the heads of the wave.  Register e of this
-        // lane holds key ks0 + 4hf + off(e), off(e) = 8(e/4) + e%4, of row q; with
-        // dq0 = q - ks0 - 4hf the test is one unsigned compare, allowed = (dq0 - off) < lim with
-        // lim = W for ordinary keys and 2^31 for sink keys (any q >= k).  Which form applies is
-        // wave-uniform.
-        f32x16 bias = f32x16{};
-        if (!tile_full(ks0, qw, W, S)) {
+        // S^T = K Q^T for every head of the wave (the K fragment is shared).  Masked tiles start
+        // the accumulator from an additive bias, 0 (allowed) or -inf (masked), shared by the
+        // heads.  Register e of this lane holds key ks0 + 4hf + off(e), off(e) = 8(e/4) + e%4,
+        // of row q; with dq0 = q - ks0 - 4hf the test is one unsigned compare,
+        // allowed = (dq0 - off) < lim, lim = W for ordinary keys and 2^31 for sink keys (any
+        // q >= k).  Which form applies is wave-uniform.
+        f32x16 s[HPW];
+        auto qk = [&](const f32x16& c0) {
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            const u32x4 kf = *reinterpret_cast<const u32x4*>(Kl + (32 * sb + r32) * KROW + hf * (D / 2) + 8 * ks);
+#pragma unroll
+            for (int h = 0; h < HPW; ++h) s[h] = E::mfma(kf, qf[h][ks], ks == 0 ? c0 : s[h]);
+          }
+        };
+        if (tile_full(ks0, qw, W, S)) {
+          qk(f32x16{});
+        } else {
+          f32x16 bias;
           const int dq0 = q - ks0 - 4 * hf;
           if (ks0 >= S || ks0 + 32 <= S) {  // one limit for all 32 keys
             const unsigned lim = ks0 >= S ? unsigned(W) : 0x80000000u;
@@ -166,33 +173,36 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
               bias[e] = unsigned(dq0 - off) < (off < sl ? 0x80000000u : unsigned(W)) ? 0.f : kNegInf;
             }
           }
+          qk(bias);
         }
-        // S^T = K Q^T for every head of the wave (the K fragment is shared).
-        f32x16 s[HPW];
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(Kl + (32 * sb + r32) * KROW + hf * (D / 2) + 8 * ks);
-#pragma unroll
-          for (int h = 0; h < HPW; ++h) s[h] = E::mfma(kf, qf[h][ks], ks == 0 ? bias : s[h]);
-        }
-        u32x4 pb[HPW][2];
+        float mx[HPW];
 #pragma unroll
         for (int h = 0; h < HPW; ++h) {
-          float mx = s[h][0];
+          float m = s[h][0];
 #pragma unroll
-          for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s[h][e]);
-          mx = max_halves(mx) * a.c;  // row max in the log2 domain (-inf stays -inf)
-          // Lazy rescaling: the exponent reference m2 moves only when some row's maximum exceeds
-          // it by more than kRescaleGap, so P <= 2^kRescaleGap and the rescale of the
-          // accumulators is skipped on most steps.  Results are the same up to rounding.
-          if (wave_any(mx > m2[h] + kRescaleGap)) {
-            const float mnew = fmaxf(m2[h], mx);
+          for (int e = 1; e < 16; ++e) m = fmaxf(m, s[h][e]);
+          mx[h] = max_halves(m) * a.c;  // row max in the log2 domain (-inf stays -inf)
+        }
+        // Lazy rescaling: the exponent reference m2 moves only when some row's maximum exceeds
+        // it by more than kRescaleGap, so P <= 2^kRescaleGap and the rescale of the accumulators
+        // is skipped on most steps.  Results are the same up to rounding.
+        bool grow = false;
+#pragma unroll
+        for (int h = 0; h < HPW; ++h) grow |= mx[h] > m2[h] + kRescaleGap;
+        if (wave_any(grow)) {
+#pragma unroll
+          for (int h = 0; h < HPW; ++h) {
+            const float mnew = fmaxf(m2[h], mx[h]);
             const float alpha = mnew == kNegInf ? 1.f : fast_exp2(m2[h] - mnew);
             m2[h] = mnew;
             lsum[h] *= alpha;
 #pragma unroll
             for (int db = 0; db < DB; ++db) acc[h][db] *= alpha;
           }
+        }
+        u32x4 pb[HPW][2];
+#pragma unroll
+        for (int h = 0; h < HPW; ++h) {
           const float ms = m2[h] == kNegInf ? 0.f : m2[h];
           float sv[16];
 #pragma unroll
@@ -205,15 +215,13 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
 #pragma unroll
           for (int w = 0; w < 4; ++w) lsum[h] = E::sum2(pb[h][1][w], lsum[h]);
         }
-        // O^T += V^T P^T (the V^T fragment is shared by the heads).
-        const int vrow = sigma32(r32);
+        // O^T += V^T P^T (the V^T fragment is shared by the heads): V^T read transposed from
+        // the row-major V block, keys in the row order of the P^T C tile.
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            u32x4 vf = zero16();
-            if (D >= 32 || vrow < D)
-              vf = *reinterpret_cast<const u32x4*>(Vl + (32 * db + vrow) * VROW + 32 * sb + 16 * t + 8 * hf);
+            const u32x4 vf = tr_frag<KROW>(Vl, 32 * sb + 16 * t, 32 * db, D);
 #pragma unroll
             for (int h = 0; h < HPW; ++h) acc[h][db] = E::mfma(vf, pb[h][t], acc[h][db]);
           }

@@ -168,6 +168,18 @@ def test_check_bwd_rejects_slices_beyond_32bit_offsets():
     assert L.fa_check_bwd(ctypes.byref(wide)) == _lib.FA_ERR_OVERFLOW
 
 
+def test_check_rejects_kv_slices_beyond_32bit_offsets():
+    """K and V are staged through buffer resources with 32-bit byte offsets inside one
+    (batch, KV head) slice; both entry points refuse a slice spanning 2^31 bytes or more."""
+    L = _lib.lib()
+    big = 1 << 20
+    assert L.fa_check_fwd(ctypes.byref(_fwd_params(seqlen=big))) == _lib.FA_OK
+    wide = (2 * big * 8192, big * 8192, 8192)  # (2^20 - 1) rows of 8192 elements: 2^34 bytes
+    for name in ("k_stride", "v_stride"):
+        assert L.fa_check_fwd(ctypes.byref(_fwd_params(seqlen=big, **{name: wide}))) == _lib.FA_ERR_OVERFLOW
+        assert L.fa_check_bwd(ctypes.byref(_bwd_params(seqlen=big, **{name: wide}))) == _lib.FA_ERR_OVERFLOW
+
+
 def test_entry_points_reject_before_any_hip_call():
     """fa_fwd / fa_bwd return the validation code for bad arguments (this runs without a GPU)."""
     L = _lib.lib()
