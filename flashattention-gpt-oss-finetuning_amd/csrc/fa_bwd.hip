@@ -29,17 +29,19 @@ namespace fa {
 // ---------------------------------------------------------------------------------------------
 // dQ (query-major).  Per wave: 32 rows x HPW heads.  Per 32-key step, with S^T = K Q^T and
 // dP^T = V dO^T in C layout (lane = query row), P and dS are per-lane elementwise, and
-// dQ^T += K^T dS^T takes dS^T straight from registers while K^T comes from LDS.
+// dQ^T += K^T dS^T takes dS^T straight from registers while K^T is read transposed from the
+// row-major K block in LDS.
 // ---------------------------------------------------------------------------------------------
 template <typename E, int D, int HPW>
 __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
   constexpr int BN = 64;
   constexpr int KS = D / 16;
   constexpr int DB = D >= 32 ? D / 32 : 1;
-  constexpr int KROW = D + 8;
-  constexpr int TROW = BN + 8;
-  constexpr int BUF = 2 * BN * KROW + D * TROW;  // K, V row-major + K^T permuted
-  constexpr int NK = (BN * D / 8 + 255) / 256;
+  constexpr int KROW = D + 8;              // K and V row stride in LDS (elements)
+  constexpr int BUF = 2 * BN * KROW;       // K, then V, both row-major [key][d]
+  constexpr int CPB = BN * D / 8;          // 16-byte chunks per 64-key block of K (or V)
+  constexpr int NK = (CPB + 255) / 256;    // chunks per thread
+  constexpr bool ALL_ON = CPB >= 256;      // every thread loads a chunk of every tile
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF];
 
   const int tid = threadIdx.x;
@@ -62,9 +64,10 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
   const bool wave_active = qw < a.L;
   const int L = a.L, W = a.W, S = a.S;
 
-  // Row operands and row statistics.
+  // Row operands and row statistics.  delta = rowsum(dO o O) is stored for the dK/dV kernel;
+  // the dP accumulator of every key tile starts from -delta, so dS = P * acc.
   u32x4 qf[HPW][KS], dof[HPW][KS];
-  float lse2[HPW], delta[HPW];
+  float lse2[HPW], ndelta[HPW];
 #pragma unroll
   for (int h = 0; h < HPW; ++h) {
     const char* qp = reinterpret_cast<const char*>(a.q) +
@@ -87,11 +90,12 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
       dof[h][ks] = dv;
       dsum += dot8<E>(dv, ov);
     }
-    delta[h] = dsum + xor32(dsum);
+    const float delta = sum_halves(dsum);
+    ndelta[h] = -delta;
     lse2[h] = __builtin_inff();
     if (q < L) {
       lse2[h] = a.lse[int64_t(b) * a.slse[0] + int64_t(hw + h) * a.slse[1] + int64_t(q) * a.slse[2]] * kLog2e;
-      if (hf == 0) a.delta[(int64_t(b) * a.Hq + hw + h) * a.Lp + q] = delta[h];
+      if (hf == 0) a.delta[(int64_t(b) * a.Hq + hw + h) * a.Lp + q] = delta;
     }
   }
 
@@ -103,22 +107,32 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
 
   const QPlan plan = qplan(q0, BM, L, W, S);
 
-  const char* kbase = reinterpret_cast<const char*>(a.k) + 2 * (int64_t(b) * a.sk[0] + int64_t(kvh) * a.sk[1]);
-  const char* vbase = reinterpret_cast<const char*>(a.v) + 2 * (int64_t(b) * a.sv[0] + int64_t(kvh) * a.sv[1]);
+  // K/V of the KV head through buffer resources spanning rows [0, L): rows past L read as zero
+  // (a slice is < 2^31 bytes, checked by the C ABI).
+  const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * (int64_t(b) * a.sk[0] + int64_t(kvh) * a.sk[1]),
+                              span_bytes(L, a.sk[2], D));
+  const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * (int64_t(b) * a.sv[0] + int64_t(kvh) * a.sv[1]),
+                              span_bytes(L, a.sv[2], D));
+  uint32_t off_k[NK], off_v[NK];
+  int off_l[NK];
+#pragma unroll
+  for (int it = 0; it < NK; ++it) {
+    const int c = tid + 256 * it;
+    const int row = c / (D / 8), col = c % (D / 8);
+    off_k[it] = uint32_t((int64_t(row) * a.sk[2] + 8 * col) * 2);
+    off_v[it] = uint32_t((int64_t(row) * a.sv[2] + 8 * col) * 2);
+    off_l[it] = row * KROW + 8 * col;
+  }
+  const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
 
   u32x4 kreg[NK], vreg[NK];
   auto gload = [&](int kb) {
 #pragma unroll
     for (int it = 0; it < NK; ++it) {
-      const int c = tid + 256 * it;
-      const int row = c / (D / 8), col = c % (D / 8);
-      u32x4 kv = zero16(), vv = zero16();
-      if (c < BN * D / 8 && kb + row < L) {
-        kv = ld16(kbase + 2 * (int64_t(kb + row) * a.sk[2] + 8 * col));
-        vv = ld16(vbase + 2 * (int64_t(kb + row) * a.sv[2] + 8 * col));
+      if (ALL_ON || tid + 256 * it < CPB) {
+        kreg[it] = buf_ld16(rk, off_k[it] + uint32_t(kb) * bk);
+        vreg[it] = buf_ld16(rv, off_v[it] + uint32_t(kb) * bv);
       }
-      kreg[it] = kv;
-      vreg[it] = vv;
     }
   };
   auto sstore = [&](int buf) {
@@ -126,36 +140,15 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
     uint16_t* Vl = Kl + BN * KROW;
 #pragma unroll
     for (int it = 0; it < NK; ++it) {
-      const int c = tid + 256 * it;
-      const int row = c / (D / 8), col = c % (D / 8);
-      if (c < BN * D / 8) {
-        st16(Kl + row * KROW + 8 * col, kreg[it]);
-        st16(Vl + row * KROW + 8 * col, vreg[it]);
+      if (ALL_ON || tid + 256 * it < CPB) {
+        st16(Kl + off_l[it], kreg[it]);
+        st16(Vl + off_l[it], vreg[it]);
       }
-    }
-  };
-  auto tstore = [&](int buf) {
-    // K^T (permuted key order) from the K rows just written to LDS: thread tid < 2*D owns one
-    // unit of 4 keys x 8 head-dim indices.
-    const uint16_t* Kl = lds + buf * BUF;
-    uint16_t* Tl = lds + buf * BUF + 2 * BN * KROW;
-    if (tid < 2 * D) {
-      const int dc = tid % (D / 8), kq = tid / (D / 8);
-      u32x4 rows[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) rows[r] = *reinterpret_cast<const u32x4*>(Kl + (4 * kq + r) * KROW + 8 * dc);
-      u32x2 cols[8];
-      transpose4x8(rows, cols);
-      const int pos = perm_pos(4 * kq);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x2*>(Tl + (8 * dc + i) * TROW + pos) = cols[i];
     }
   };
 
   gload(qplan_block(plan, 0));
   sstore(0);
-  __syncthreads();
-  tstore(0);
   __syncthreads();
 
   for (int i = 0; i < plan.nb; ++i) {
@@ -165,63 +158,77 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
     if (wave_active) {
       const uint16_t* Kl = lds + (i & 1) * BUF;
       const uint16_t* Vl = Kl + BN * KROW;
-      const uint16_t* Tl = Kl + 2 * BN * KROW;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
         const int ks0 = kb + 32 * sb;
         if (!wave_needs(ks0, qw, L, W, S)) continue;
-        f32x16 s[HPW], dp[HPW];
-#pragma unroll
-        for (int h = 0; h < HPW; ++h) {
-          s[h] = f32x16{};
-          dp[h] = f32x16{};
-        }
+        // S^T = K Q^T and dP^T - delta = V dO^T - delta for every head (K/V fragments shared).
+        // Masked tiles start S^T from an additive bias, 0 (allowed) or -inf (masked), so P is
+        // exactly 0 there; the test is the forward's: register e holds key ks0 + 4hf + off(e),
+        // allowed = (dq0 - off) < lim.
+        u32x4 kf[KS], vf[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           const int off = (32 * sb + r32) * KROW + hf * (D / 2) + 8 * ks;
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(Kl + off);
-          const u32x4 vf = *reinterpret_cast<const u32x4*>(Vl + off);
+          kf[ks] = *reinterpret_cast<const u32x4*>(Kl + off);
+          vf[ks] = *reinterpret_cast<const u32x4*>(Vl + off);
+        }
+        f32x16 s[HPW], dp[HPW];
+        auto qk = [&](const f32x16& c0) {
 #pragma unroll
           for (int h = 0; h < HPW; ++h) {
-            s[h] = E::mfma(kf, qf[h][ks], s[h]);
-            dp[h] = E::mfma(vf, dof[h][ks], dp[h]);
+            f32x16 d0;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) d0[e] = ndelta[h];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+              s[h] = E::mfma(kf[ks], qf[h][ks], ks == 0 ? c0 : s[h]);
+              dp[h] = E::mfma(vf[ks], dof[h][ks], ks == 0 ? d0 : dp[h]);
+            }
           }
+        };
+        if (tile_full(ks0, qw, W, S)) {
+          qk(f32x16{});
+        } else {
+          f32x16 bias;
+          const int dq0 = q - ks0 - 4 * hf;
+          if (ks0 >= S || ks0 + 32 <= S) {  // one limit for all 32 keys
+            const unsigned lim = ks0 >= S ? unsigned(W) : 0x80000000u;
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              bias[e] = unsigned(dq0 - (8 * (e / 4) + (e % 4))) < lim ? 0.f : kNegInf;
+          } else {  // the sink boundary S falls inside these keys
+            const int sl = S - ks0 - 4 * hf;  // keys with off < sl are sinks
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int off = 8 * (e / 4) + (e % 4);
+              bias[e] = unsigned(dq0 - off) < (off < sl ? 0x80000000u : unsigned(W)) ? 0.f : kNegInf;
+            }
+          }
+          qk(bias);
         }
-        const bool full = tile_full(ks0, qw, W, S);
-        u32x4 dsb[HPW][2];
+        // K^T operands of dQ^T += K^T dS^T, shared by the heads: read transposed from the
+        // row-major K block, keys in the row order of the dS^T C tile.
+        u32x4 kt[DB][2];
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) kt[db][t] = tr_frag<KROW>(Kl, 32 * sb + 16 * t, 32 * db, D);
 #pragma unroll
         for (int h = 0; h < HPW; ++h) {
           float ds[16];
-          const int kl = ks0 + 4 * hf;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int off = 8 * (e / 4) + (e % 4);
-            float p = fast_exp2(fmaf(s[h][e], a.c, -lse2[h]));
-            p = (full | allowed(q - kl - off, kl + off, W, S)) ? p : 0.f;
-            ds[e] = p * (dp[h][e] - delta[h]);
-          }
-          dsb[h][0] = pack8<E>(ds);
-          dsb[h][1] = pack8<E>(ds + 8);
-        }
-        const int trow = sigma32(r32);
+          for (int e = 0; e < 16; ++e) ds[e] = fast_exp2(fmaf(s[h][e], a.c, -lse2[h])) * dp[h][e];
+          const u32x4 d0 = pack8<E>(ds), d1 = pack8<E>(ds + 8);
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            u32x4 kt = zero16();
-            if (D >= 32 || trow < D)
-              kt = *reinterpret_cast<const u32x4*>(Tl + (32 * db + trow) * TROW + 32 * sb + 16 * t + 8 * hf);
-#pragma unroll
-            for (int h = 0; h < HPW; ++h) acc[h][db] = E::mfma(kt, dsb[h][t], acc[h][db]);
+          for (int db = 0; db < DB; ++db) {
+            acc[h][db] = E::mfma(kt[db][0], d0, acc[h][db]);
+            acc[h][db] = E::mfma(kt[db][1], d1, acc[h][db]);
           }
         }
       }
     }
-    if (more) {
-      sstore((i + 1) & 1);
-      __syncthreads();
-      tstore((i + 1) & 1);
-    }
+    if (more) sstore((i + 1) & 1);
     __syncthreads();
   }
 

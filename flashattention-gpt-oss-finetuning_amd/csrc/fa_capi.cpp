@@ -51,10 +51,11 @@ int check_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t L, int32_t D, int32
 }
 
 // Workgroup shape of the query-major kernels: wq waves along the sequence x wh waves along the
-// heads, each wave 32 rows x hpw heads; hpw * wh heads must divide the group size so that a
-// workgroup never straddles two KV heads.
-void choose_qmajor(int G, int D, int* hpw, int* wh, int* wq) {
-  const int hmax = D <= 64 ? 2 : 1;
+// heads, each wave 32 rows x hpw heads (hpw <= hmax); hpw * wh heads must divide the group size
+// so that a workgroup never straddles two KV heads.  The forward shares each K/V fragment
+// between two heads of a wave for D <= 64; the dQ kernel keeps one head per wave, which leaves
+// it two waves per SIMD (measured faster at D = 64).
+void choose_qmajor(int G, int hmax, int* hpw, int* wh, int* wq) {
   for (int h = hmax; h >= 1; --h)
     for (int w = 4; w >= 1; w /= 2)
       if (G % (h * w) == 0) {
@@ -178,7 +179,7 @@ int fa_fwd(const fa_fwd_params* p, void* stream) {
   copy3(a.so_out, p->o_stride);
   copy3(a.slse, p->lse_stride);
   int hpw, wh, wq;
-  choose_qmajor(a.G, p->head_dim, &hpw, &wh, &wq);
+  choose_qmajor(a.G, p->head_dim <= 64 ? 2 : 1, &hpw, &wh, &wq);
   a.wh = wh;
   a.wq = wq;
   a.n_qtiles = (a.L + 32 * wq - 1) / (32 * wq);
@@ -229,7 +230,7 @@ int prepare_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
   a.delta = static_cast<float*>(workspace);
 
   int wh, wq;
-  choose_qmajor(a.G, p->head_dim, hpw, &wh, &wq);
+  choose_qmajor(a.G, 1, hpw, &wh, &wq);
   a.wh = wh;
   a.wq = wq;
   a.n_qtiles = (a.L + 32 * wq - 1) / (32 * wq);

@@ -140,20 +140,24 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
       for (int sb = 0; sb < 2; ++sb) {
         const int ks0 = kb + 32 * sb;
         if (!wave_needs(ks0, qw, L, W, S)) continue;
-        // S^T = K Q^T for every head of the wave (the K fragment is shared).  Masked tiles start
+        // S^T = K Q^T for every head of the wave (the K fragments are shared).  Masked tiles start
         // the accumulator from an additive bias, 0 (allowed) or -inf (masked), shared by the
         // heads.  Register e of this lane holds key ks0 + 4hf + off(e), off(e) = 8(e/4) + e%4,
         // of row q; with dq0 = q - ks0 - 4hf the test is one unsigned compare,
         // allowed = (dq0 - off) < lim, lim = W for ordinary keys and 2^31 for sink keys (any
         // q >= k).  Which form applies is wave-uniform.
         f32x16 s[HPW];
+        // Head by head: head 0's scores are complete while head 1's MFMAs are still in the
+        // pipe, and head 0's softmax (VALU) overlaps them.
+        u32x4 kf[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          kf[ks] = *reinterpret_cast<const u32x4*>(Kl + (32 * sb + r32) * KROW + hf * (D / 2) + 8 * ks);
         auto qk = [&](const f32x16& c0) {
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) {
-            const u32x4 kf = *reinterpret_cast<const u32x4*>(Kl + (32 * sb + r32) * KROW + hf * (D / 2) + 8 * ks);
+          for (int h = 0; h < HPW; ++h)
 #pragma unroll
-            for (int h = 0; h < HPW; ++h) s[h] = E::mfma(kf, qf[h][ks], ks == 0 ? c0 : s[h]);
-          }
+            for (int ks = 0; ks < KS; ++ks) s[h] = E::mfma(kf[ks], qf[h][ks], ks == 0 ? c0 : s[h]);
         };
         if (tile_full(ks0, qw, W, S)) {
           qk(f32x16{});
@@ -175,56 +179,45 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
           }
           qk(bias);
         }
-        float mx[HPW];
+        // V^T operands of O^T += V^T P^T, shared by the heads: read transposed from the
+        // row-major V block, keys in the row order of the P^T C tile.
+        u32x4 vf[DB][2];
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) vf[db][t] = tr_frag<KROW>(Vl, 32 * sb + 16 * t, 32 * db, D);
 #pragma unroll
         for (int h = 0; h < HPW; ++h) {
           float m = s[h][0];
 #pragma unroll
           for (int e = 1; e < 16; ++e) m = fmaxf(m, s[h][e]);
-          mx[h] = max_halves(m) * a.c;  // row max in the log2 domain (-inf stays -inf)
-        }
-        // Lazy rescaling: the exponent reference m2 moves only when some row's maximum exceeds
-        // it by more than kRescaleGap, so P <= 2^kRescaleGap and the rescale of the accumulators
-        // is skipped on most steps.  Results are the same up to rounding.
-        bool grow = false;
-#pragma unroll
-        for (int h = 0; h < HPW; ++h) grow |= mx[h] > m2[h] + kRescaleGap;
-        if (wave_any(grow)) {
-#pragma unroll
-          for (int h = 0; h < HPW; ++h) {
-            const float mnew = fmaxf(m2[h], mx[h]);
+          const float mx = max_halves(m) * a.c;  // row max in the log2 domain (-inf stays -inf)
+          // Lazy rescaling: the exponent reference m2 moves only when some row's maximum
+          // exceeds it by more than kRescaleGap, so P <= 2^kRescaleGap and the rescale of the
+          // accumulators is skipped on most steps.  Results are the same up to rounding.
+          if (wave_any(mx > m2[h] + kRescaleGap)) {
+            const float mnew = fmaxf(m2[h], mx);
             const float alpha = mnew == kNegInf ? 1.f : fast_exp2(m2[h] - mnew);
             m2[h] = mnew;
             lsum[h] *= alpha;
 #pragma unroll
             for (int db = 0; db < DB; ++db) acc[h][db] *= alpha;
           }
-        }
-        u32x4 pb[HPW][2];
-#pragma unroll
-        for (int h = 0; h < HPW; ++h) {
           const float ms = m2[h] == kNegInf ? 0.f : m2[h];
           float sv[16];
 #pragma unroll
           for (int e = 0; e < 16; ++e) sv[e] = fast_exp2(fmaf(s[h][e], a.c, -ms));
-          pb[h][0] = pack8<E>(sv);
-          pb[h][1] = pack8<E>(sv + 8);
+          const u32x4 pb0 = pack8<E>(sv), pb1 = pack8<E>(sv + 8);
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            acc[h][db] = E::mfma(vf[db][0], pb0, acc[h][db]);
+            acc[h][db] = E::mfma(vf[db][1], pb1, acc[h][db]);
+          }
           // the row sum adds the 16-bit P that the PV product uses
 #pragma unroll
-          for (int w = 0; w < 4; ++w) lsum[h] = E::sum2(pb[h][0][w], lsum[h]);
+          for (int w = 0; w < 4; ++w) lsum[h] = E::sum2(pb0[w], lsum[h]);
 #pragma unroll
-          for (int w = 0; w < 4; ++w) lsum[h] = E::sum2(pb[h][1][w], lsum[h]);
-        }
-        // O^T += V^T P^T (the V^T fragment is shared by the heads): V^T read transposed from
-        // the row-major V block, keys in the row order of the P^T C tile.
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const u32x4 vf = tr_frag<KROW>(Vl, 32 * sb + 16 * t, 32 * db, D);
-#pragma unroll
-            for (int h = 0; h < HPW; ++h) acc[h][db] = E::mfma(vf, pb[h][t], acc[h][db]);
-          }
+          for (int w = 0; w < 4; ++w) lsum[h] = E::sum2(pb1[w], lsum[h]);
         }
       }
     }
