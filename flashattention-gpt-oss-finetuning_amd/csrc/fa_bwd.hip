@@ -37,8 +37,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
   constexpr int BN = 64;
   constexpr int KS = D / 16;
   constexpr int DB = D >= 32 ? D / 32 : 1;
-  constexpr int KROW = D + 8;              // K and V row stride in LDS (elements)
-  constexpr int BUF = 2 * BN * KROW;       // K, then V, both row-major [key][d]
+  constexpr int BUF = 2 * BN * D;          // K, then V, both swizzled row-major [key][d]
   constexpr int CPB = BN * D / 8;          // 16-byte chunks per 64-key block of K (or V)
   constexpr int NK = (CPB + 255) / 256;    // chunks per thread
   constexpr bool ALL_ON = CPB >= 256;      // every thread loads a chunk of every tile
@@ -121,7 +120,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
     const int row = c / (D / 8), col = c % (D / 8);
     off_k[it] = uint32_t((int64_t(row) * a.sk[2] + 8 * col) * 2);
     off_v[it] = uint32_t((int64_t(row) * a.sv[2] + 8 * col) * 2);
-    off_l[it] = row * KROW + 8 * col;
+    off_l[it] = swz_off<D>(row, 8 * col);
   }
   const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
 
@@ -137,7 +136,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
   };
   auto sstore = [&](int buf) {
     uint16_t* Kl = lds + buf * BUF;
-    uint16_t* Vl = Kl + BN * KROW;
+    uint16_t* Vl = Kl + BN * D;
 #pragma unroll
     for (int it = 0; it < NK; ++it) {
       if (ALL_ON || tid + 256 * it < CPB) {
@@ -157,7 +156,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
     if (more) gload(qplan_block(plan, i + 1));
     if (wave_active) {
       const uint16_t* Kl = lds + (i & 1) * BUF;
-      const uint16_t* Vl = Kl + BN * KROW;
+      const uint16_t* Vl = Kl + BN * D;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
         const int ks0 = kb + 32 * sb;
@@ -169,7 +168,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
         u32x4 kf[KS], vf[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const int off = (32 * sb + r32) * KROW + hf * (D / 2) + 8 * ks;
+          const int off = swz_off<D>(32 * sb + r32, hf * (D / 2) + 8 * ks);
           kf[ks] = *reinterpret_cast<const u32x4*>(Kl + off);
           vf[ks] = *reinterpret_cast<const u32x4*>(Vl + off);
         }
@@ -213,7 +212,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
-          for (int t = 0; t < 2; ++t) kt[db][t] = tr_frag<KROW>(Kl, 32 * sb + 16 * t, 32 * db, D);
+          for (int t = 0; t < 2; ++t) kt[db][t] = tr_frag_swz<D>(Kl, 32 * sb + 16 * t, 32 * db, D);
 #pragma unroll
         for (int h = 0; h < HPW; ++h) {
           float ds[16];
@@ -268,8 +267,7 @@ template <typename E, int D>
 __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   constexpr int KS = D / 16;
   constexpr int DB = D >= 32 ? D / 32 : 1;
-  constexpr int ROW = D + 8;                 // tile row stride (elements)
-  constexpr int TILE = 32 * ROW;             // 32 rows of Q or dO
+  constexpr int TILE = 32 * D;               // 32 rows of Q or dO, swizzled row-major
   constexpr int SLOT = 2 * TILE + 128;       // Q, dO, then lse2[32] and delta[32] as fp32
   constexpr int STAGE = 2 * SLOT;            // two items per step
   constexpr int CPR = D / 8;                 // 16-byte chunks per row
@@ -360,7 +358,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
     lane_on[i] = ALL_ON || wc < TPI;
     lane_off_q[i] = uint32_t((int64_t(row) * a.sq[2] + 8 * col) * 2);
     lane_off_d[i] = uint32_t((int64_t(row) * a.sdo[2] + 8 * col) * 2);
-    lane_lds[i] = row * ROW + 8 * col;
+    lane_lds[i] = swz_off<D>(row, 8 * col);
   }
   const char* qslice = reinterpret_cast<const char*>(a.q) + 2 * (int64_t(b) * a.sq[0] + int64_t(kvh) * G * a.sq[1]);
   const char* dslice = reinterpret_cast<const char*>(a.dout) + 2 * (int64_t(b) * a.sdo[0] + int64_t(kvh) * G * a.sdo[1]);
@@ -434,7 +432,6 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   //   regular workgroup: q - k < lim, lim = W for ordinary keys, 2^31 for sink keys (any
   //     q >= k), wqhi - k for sink keys of a block whose later rows belong to chunk workgroups;
   //   chunk workgroup: q - qlo < lim, lim = qhi - qlo for sink keys, 0 for the others.
-  const int a_off = r32 * ROW + hf * (D / 2);
   unsigned lim;
   if (is_chunk) lim = key < S ? unsigned(qhi - qlo) : 0u;
   else lim = key < S ? (partial_block ? unsigned(max(wqhi - key, 0)) : 0x80000000u) : unsigned(W);
@@ -458,8 +455,9 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
     }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      sacc = E::mfma(lds16(Qt + a_off + 8 * ks), kf[ks], sacc);
-      dpacc = E::mfma(lds16(Dt + a_off + 8 * ks), vf[ks], dpacc);  // dP - delta
+      const int a_off = swz_off<D>(r32, hf * (D / 2) + 8 * ks);
+      sacc = E::mfma(lds16(Qt + a_off), kf[ks], sacc);
+      dpacc = E::mfma(lds16(Dt + a_off), vf[ks], dpacc);  // dP - delta
     }
     const bool full = !is_chunk && qr0 >= wqlo && qr0 + 32 <= wqhi && tile_full(ks0, qr0, W, S);
     const int m0 = qr0 + 4 * hf - mref;  // mask coordinate of register e = 0
@@ -488,8 +486,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const u32x4 dt = tr_frag<ROW>(Dt, 16 * t, 32 * db, D);
-        const u32x4 qt = tr_frag<ROW>(Qt, 16 * t, 32 * db, D);
+        const u32x4 dt = tr_frag_swz<D>(Dt, 16 * t, 32 * db, D);
+        const u32x4 qt = tr_frag_swz<D>(Qt, 16 * t, 32 * db, D);
         dv[db] = E::mfma(dt, t ? pb1 : pb0, dv[db]);
         dk[db] = E::mfma(qt, t ? sb1 : sb0, dk[db]);
       }

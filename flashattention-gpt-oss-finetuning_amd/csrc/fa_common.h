@@ -164,6 +164,40 @@ __device__ __forceinline__ u32x4 tr_frag(const uint16_t* tile, int r0, int col0,
   return r;
 }
 
+// Swizzled [rows][D] tiles of 16-bit values in LDS (row stride D, no padding): chunk j (8
+// elements, 16 bytes) of row r is stored at chunk j ^ swz(r).  With 128 bytes per LDS cycle
+// (32 banks of 4 bytes) the swizzle keeps both access patterns of the kernels conflict-free:
+//  * 16-byte row reads (A operands: 8 consecutive rows, one chunk each) -- swz takes distinct
+//    values on any 8 rows that share a bank cycle;
+//  * ds_read_b64_tr_b16 (4 consecutive rows, chunks j and j ^ 2) -- swz(r) ^ swz(r') is never 0
+//    or 2 for two rows of an aligned group of 4.
+// swz(r + 8) = swz(r), so a tile read at rows r and r + 8 uses one base address.
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (D >= 64) return (r & 1) | ((r & 2) << 1) | ((r & 4) >> 1);
+  else if constexpr (D == 32) return (r >> 1) & 3;
+  else return (r >> 2) & 1;
+}
+// element offset of (row r, element column col) in a swizzled tile
+template <int D>
+__device__ __forceinline__ int swz_off(int r, int col) {
+  return r * D + (((col >> 3) ^ swz<D>(r)) << 3) + (col & 7);
+}
+
+// tr_frag on a swizzled [rows][D] tile (see swz): the same operand, conflict-free.
+template <int D>
+__device__ __forceinline__ u32x4 tr_frag_swz(const uint16_t* tile, int r0, int col0, int ncols) {
+  const int lane = threadIdx.x & 63;
+  const int s = lane & 15, rh = (lane >> 4) & 1, hf = lane >> 5;
+  int col = col0 + sigma32(16 * rh + 4 * (s & 3));
+  if (col >= ncols) col = 0;  // any valid address; those lanes are zeroed below
+  const uint16_t* p = tile + swz_off<D>(r0 + 4 * hf + (s >> 2), col);
+  const u32x2 lo = ds_read_tr16(p), hi = ds_read_tr16(p + 8 * D);
+  u32x4 r = {lo[0], lo[1], hi[0], hi[1]};
+  if (col0 + sigma32(lane & 31) >= ncols) r = zero16();
+  return r;
+}
+
 // Exchange with the lane 32 positions away (the other half of the wave).
 __device__ __forceinline__ float xor32(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(

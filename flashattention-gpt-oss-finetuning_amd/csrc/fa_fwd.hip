@@ -28,8 +28,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   constexpr int BN = 64;                   // keys per LDS block
   constexpr int KS = D / 16;               // reduction steps over the head dim
   constexpr int DB = D >= 32 ? D / 32 : 1; // 32-row C tiles of O^T
-  constexpr int KROW = D + 8;              // K and V row stride in LDS (elements)
-  constexpr int BUF = 2 * BN * KROW;       // K, then V, both row-major [key][d]
+  constexpr int BUF = 2 * BN * D;          // K, then V, both swizzled row-major [key][d]
   constexpr int CPB = BN * D / 8;          // 16-byte chunks per 64-key block of K (or V)
   constexpr int NK = (CPB + 255) / 256;    // chunks per thread
   constexpr bool ALL_ON = CPB >= 256;      // every thread loads a chunk of every tile
@@ -98,7 +97,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     const int row = c / (D / 8), col = c % (D / 8);
     off_k[it] = uint32_t((int64_t(row) * a.sk[2] + 8 * col) * 2);
     off_v[it] = uint32_t((int64_t(row) * a.sv[2] + 8 * col) * 2);
-    off_l[it] = row * KROW + 8 * col;
+    off_l[it] = swz_off<D>(row, 8 * col);
   }
   const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
 
@@ -115,7 +114,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   };
   auto sstore = [&](int buf) {
     uint16_t* Kl = lds + buf * BUF;
-    uint16_t* Vl = Kl + BN * KROW;
+    uint16_t* Vl = Kl + BN * D;
 #pragma unroll
     for (int it = 0; it < NK; ++it) {
       if (ALL_ON || tid + 256 * it < CPB) {
@@ -135,7 +134,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     if (more) gload(qplan_block(plan, i + 1));
     if (wave_active) {
       const uint16_t* Kl = lds + (i & 1) * BUF;
-      const uint16_t* Vl = Kl + BN * KROW;
+      const uint16_t* Vl = Kl + BN * D;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
         const int ks0 = kb + 32 * sb;
@@ -152,7 +151,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
         u32x4 kf[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
-          kf[ks] = *reinterpret_cast<const u32x4*>(Kl + (32 * sb + r32) * KROW + hf * (D / 2) + 8 * ks);
+          kf[ks] = *reinterpret_cast<const u32x4*>(Kl + swz_off<D>(32 * sb + r32, hf * (D / 2) + 8 * ks));
         auto qk = [&](const f32x16& c0) {
 #pragma unroll
           for (int h = 0; h < HPW; ++h)
@@ -185,7 +184,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
-          for (int t = 0; t < 2; ++t) vf[db][t] = tr_frag<KROW>(Vl, 32 * sb + 16 * t, 32 * db, D);
+          for (int t = 0; t < 2; ++t) vf[db][t] = tr_frag_swz<D>(Vl, 32 * sb + 16 * t, 32 * db, D);
 #pragma unroll
         for (int h = 0; h < HPW; ++h) {
           float m = s[h][0];
