@@ -37,9 +37,10 @@ struct Args {
   // KV-major kernel (dK/dV)
   int n_kblocks;     // ceil(L / 64)
   int nsp;           // leading 64-key blocks whose sink rows are split into chunks
-  int n_chunks;      // chunks of chunk_rows query rows (0 when nsp == 0)
+  int n_chunks;      // chunks of chunk_rows query rows per chunked block (0 when nsp == 0)
   int chunk_rows;
   int n_chunk_wgs;   // B * Hkv * nsp * n_chunks
+  int srows;         // sink rows stored per block in the partial sums: min(S, 64)
 };
 
 // Launchers (return the hipError_t of the launch; launch_bwd_dkdv also launches the sink fold).

@@ -281,25 +281,24 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   const int kh = wave & 1, hh = wave >> 1;
   const int L = a.L, W = a.W, S = a.S, G = a.G;
 
-  int id = xcd_remap(blockIdx.x, gridDim.x);
-  int b, kvh, kblk, chunk = -1, qlo, qhi;
-  if (id < a.n_chunk_wgs) {
-    chunk = id % a.n_chunks;
-    int t = id / a.n_chunks;
-    kblk = t % a.nsp;
-    t /= a.nsp;
-    kvh = t % a.Hkv;
-    b = t / a.Hkv;
-    qlo = kv_chunk_lo(kblk, chunk, a.chunk_rows, L, W);
-    qhi = kv_chunk_hi(chunk, a.chunk_rows, L);
-  } else {
-    id -= a.n_chunk_wgs;
-    kblk = id % a.n_kblocks;
-    const int t = id / a.n_kblocks;
-    kvh = t % a.Hkv;
-    b = t / a.Hkv;
+  // Workgroups come in groups per (b, KV head): the n_kblocks regular ones, then the sink
+  // chunks.  A group's workgroups land on one XCD (they share its L2), and the short chunk
+  // workgroups run last, filling the slots that the regular ones leave.
+  const int per_group = a.n_kblocks + a.nsp * a.n_chunks;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int grp = id / per_group, r = id % per_group;
+  const int kvh = grp % a.Hkv, b = grp / a.Hkv;
+  int kblk, chunk = -1, qlo, qhi;
+  if (r < a.n_kblocks) {
+    kblk = r;
     qlo = kKvKeys * kblk;
     qhi = kv_window_end(kblk, L, W);
+  } else {
+    const int t = r - a.n_kblocks;
+    kblk = t % a.nsp;
+    chunk = t / a.nsp;
+    qlo = kv_chunk_lo(kblk, chunk, a.chunk_rows, L, W);
+    qhi = kv_chunk_hi(kblk, chunk, a.chunk_rows, L, W);
   }
   const bool is_chunk = chunk >= 0;
   const bool partial_block = kblk < a.nsp;
@@ -552,7 +551,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   if (partial_block) {
     const int64_t blk = (int64_t(b) * a.Hkv + kvh) * a.nsp + kblk;
     const int slot = is_chunk ? chunk : a.n_chunks;
-    pk = a.partial + (blk * (a.n_chunks + 1) + slot) * 2 * kKvKeys * D;
+    pk = a.partial + (blk * (a.n_chunks + 1) + slot) * 2 * a.srows * D;
   }
   if (hh == 0 && key < L) {
     const bool sink_row = partial_block && key < S;
@@ -561,8 +560,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
       if (D == 16 && hf == 1) continue;
       const int d0 = 32 * db + (D >= 32 ? 16 * hf : 0);
       if (sink_row) {
-        float* rk = pk + (32 * kh + r32) * D + d0;
-        float* rv = rk + kKvKeys * D;
+        float* rk = pk + (32 * kh + r32) * D + d0;  // row key - 64 kblk < srows
+        float* rv = rk + a.srows * D;
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
           *reinterpret_cast<f32x4*>(rk + 4 * e4) =
@@ -609,10 +608,10 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
   const int kvh = int(bh % a.Hkv), b = int(bh / a.Hkv);
   const int kblk = key / kKvKeys, row = key % kKvKeys;
   const int64_t blk = bh * a.nsp + kblk;
-  const float* src = a.partial + blk * (a.n_chunks + 1) * 2 * kKvKeys * D + row * D + d;
+  const float* src = a.partial + blk * (a.n_chunks + 1) * 2 * a.srows * D + row * D + d;
   // Slots are added in order; the loads of up to kBatch slots are in flight together.
   constexpr int kBatch = 16;
-  constexpr int64_t kSlot = 2 * kKvKeys * D;
+  const int64_t kSlot = int64_t(2) * a.srows * D;
   const int ns = a.n_chunks + 1;
   float sk = 0.f, sv = 0.f;
   for (int s0 = 0; s0 < ns; s0 += kBatch) {
@@ -622,7 +621,7 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
       const bool in = s0 + j < ns;
       const float* p = src + int64_t(in ? s0 + j : 0) * kSlot;
       xk[j] = in ? p[0] : 0.f;
-      xv[j] = in ? p[kKvKeys * D] : 0.f;
+      xv[j] = in ? p[a.srows * D] : 0.f;
     }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {

@@ -16,7 +16,7 @@
 namespace {
 
 constexpr int64_t kMaxSeq = int64_t(1) << 28;
-constexpr int kChunkRows = 256;  // query rows per sink-chunk workgroup of the dK/dV kernel
+constexpr int kChunkRows = 64;  // query rows per sink-chunk workgroup of the dK/dV kernel
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -70,16 +70,17 @@ void choose_qmajor(int G, int hmax, int* hpw, int* wh, int* wq) {
 }
 
 struct SinkPlan {
-  int nsp, n_chunks;
+  int nsp, n_chunks, srows;  // chunked blocks, chunks per block, stored sink rows per block
 };
 
 SinkPlan sink_plan(int L, int W, int S) {
   // clamp as the kernels do
   W = W < 0 ? 0 : (W > L ? L : W);
   S = S < 0 ? 0 : (S > L ? L : S);
-  SinkPlan p{0, 0};
+  SinkPlan p{0, 0, 0};
   p.nsp = fa::kv_sink_blocks(L, W, S);
-  if (p.nsp > 0) p.n_chunks = (L + kChunkRows - 1) / kChunkRows;
+  p.n_chunks = fa::kv_n_chunks(L, W, S, kChunkRows);
+  p.srows = S < fa::kKvKeys ? S : fa::kKvKeys;
   return p;
 }
 
@@ -90,8 +91,9 @@ size_t delta_bytes(int B, int Hq, int L) {
   return align256(size_t(B) * Hq * Lp * sizeof(float));
 }
 
+// fp32 partial sums of the sink rows: [B * Hkv][nsp][n_chunks + 1 slots][dK, dV][srows][D]
 size_t partial_bytes(int B, int Hkv, int D, const SinkPlan& sp) {
-  return align256(size_t(B) * Hkv * sp.nsp * (sp.n_chunks + 1) * 2 * fa::kKvKeys * D * sizeof(float));
+  return align256(size_t(B) * Hkv * sp.nsp * (sp.n_chunks + 1) * 2 * sp.srows * D * sizeof(float));
 }
 
 void copy3(int64_t dst[3], const int64_t src[3]) {
@@ -242,6 +244,7 @@ int prepare_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
   a.nsp = sp.nsp;
   a.n_chunks = sp.n_chunks;
   a.chunk_rows = kChunkRows;
+  a.srows = sp.srows;
   a.n_chunk_wgs = a.B * a.Hkv * a.nsp * a.n_chunks;
   *out = a;
   return FA_OK;

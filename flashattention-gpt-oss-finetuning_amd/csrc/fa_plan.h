@@ -66,10 +66,12 @@ FA_HD bool tile_full(int ks0, int qr, int W, int S) {
 // half.  The rows that can see a 32-key half [ks0, ks0 + 32) through the window are
 // [ks0, ks0 + 31 + W); the workgroup sweeps the union of its halves' ranges,
 // [kKvKeys*kblk, kv_window_end), each wave from its own first key on (a half's sink keys are
-// also seen by the rows between its own window end and the workgroup's).  For the first `nsp` blocks (those holding sink keys with
-// rows beyond kv_window_end) the remaining rows [kv_window_end, L) only see the sink keys;
-// they are split into chunks of chunk_rows handled by extra workgroups, chunk c covering
-// [max(c*chunk_rows, end), min((c+1)*chunk_rows, L)).
+// also seen by the rows between its own window end and the workgroup's).  For the first `nsp`
+// blocks (those holding sink keys with rows beyond kv_window_end) the remaining rows
+// [kv_window_end, L) only see the sink keys; they are split into chunks of chunk_rows handled by
+// extra workgroups.  Chunks are laid out from the window end rounded down to 32 rows (so a
+// chunk covers whole 32-row blocks): chunk c covers [max(base + c*chunk_rows, end),
+// min(base + (c+1)*chunk_rows, L)), base = end rounded down to a multiple of 32.
 constexpr int kKvKeys = 64;
 
 FA_HD int kv_rows_end(int ks0, int nkeys, int L, int W) { return imin(L, ks0 + nkeys - 1 + W); }
@@ -82,11 +84,15 @@ FA_HD bool kv_half_needs(int qr0, int ks0, int L, int W, int S) {
   return qr0 + 31 >= ks0 && (ks0 < S || qr0 < kv_rows_end(ks0, 32, L, W));
 }
 
+FA_HD int kv_chunk_base(int kblk, int L, int W) { return kv_window_end(kblk, L, W) / 32 * 32; }
+
 FA_HD int kv_chunk_lo(int kblk, int c, int chunk_rows, int L, int W) {
-  return imax(c * chunk_rows, kv_window_end(kblk, L, W));
+  return imax(kv_chunk_base(kblk, L, W) + c * chunk_rows, kv_window_end(kblk, L, W));
 }
 
-FA_HD int kv_chunk_hi(int c, int chunk_rows, int L) { return imin((c + 1) * chunk_rows, L); }
+FA_HD int kv_chunk_hi(int kblk, int c, int chunk_rows, int L, int W) {
+  return imin(kv_chunk_base(kblk, L, W) + (c + 1) * chunk_rows, L);
+}
 
 // Number of leading key blocks whose sink rows are chunked: blocks holding a key < S whose
 // window end is before L.  (Both conditions hold on a prefix of the blocks.)
@@ -95,6 +101,11 @@ FA_HD int kv_sink_blocks(int L, int W, int S) {
   for (int kb = 0; kKvKeys * kb < S; ++kb)
     if (kv_window_end(kb, L, W) < L) n = kb + 1;
   return n;
+}
+
+// Chunks per chunked block: enough for block 0, whose window ends first.
+FA_HD int kv_n_chunks(int L, int W, int S, int chunk_rows) {
+  return kv_sink_blocks(L, W, S) > 0 ? (L - kv_chunk_base(0, L, W) + chunk_rows - 1) / chunk_rows : 0;
 }
 
 }  // namespace fa

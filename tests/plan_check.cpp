@@ -69,7 +69,7 @@ static int check_kvmajor(int L, int W, int S, int chunk_rows) {
   std::vector<int> cnt(size_t(L) * L, 0);
   const int nkb = (L + kKvKeys - 1) / kKvKeys;
   const int nsp = kv_sink_blocks(L, W, S);
-  const int n_chunks = nsp > 0 ? (L + chunk_rows - 1) / chunk_rows : 0;
+  const int n_chunks = kv_n_chunks(L, W, S, chunk_rows);
   auto sweep = [&](int kblk, int qlo, int qhi, bool chunk) -> int {
     if (qhi <= qlo) return 0;
     for (int qb = qlo / 32; qb < (qhi + 31) / 32; ++qb) {
@@ -103,7 +103,7 @@ static int check_kvmajor(int L, int W, int S, int chunk_rows) {
     if (sweep(kblk, kKvKeys * kblk, kv_window_end(kblk, L, W), false)) return 1;
   for (int kblk = 0; kblk < nsp; ++kblk)
     for (int c = 0; c < n_chunks; ++c)
-      if (sweep(kblk, kv_chunk_lo(kblk, c, chunk_rows, L, W), kv_chunk_hi(c, chunk_rows, L), true)) return 1;
+      if (sweep(kblk, kv_chunk_lo(kblk, c, chunk_rows, L, W), kv_chunk_hi(kblk, c, chunk_rows, L, W), true)) return 1;
   for (int q = 0; q < L; ++q)
     for (int k = 0; k < L; ++k) {
       const int want = ref_allowed(q, k, W, S) ? 1 : 0;

@@ -200,11 +200,12 @@ def test_workspace_bytes():
     # the window of the sink block
     assert ws(1, 8, 2, 128, 64, 200, 4) == 8 * 128 * 4
     assert ws(1, 8, 2, 100, 64, 200, 4) == 8 * 128 * 4
-    # sink split: 1 block of 64 keys, ceil(L/256) chunks + the regular slot, dK and dV,
-    # 64 rows x D fp32 each
+    # sink split: 1 block of 64 keys; its window ends at row 191, chunks of 64 rows start at 160
+    # (rounded down to 32): ceil((4096 - 160) / 64) = 62 chunks + the regular slot, dK and dV,
+    # S = 4 sink rows x D fp32 each
     L_, D = 4096, 64
     expect_delta = 64 * 4096 * 4
-    expect_partial = 8 * 1 * (16 + 1) * 2 * 64 * D * 4
+    expect_partial = 8 * 1 * (62 + 1) * 2 * 4 * D * 4
     assert ws(1, 64, 8, L_, D, 128, 4) == expect_delta + expect_partial
     # invalid problems give 0
     assert ws(1, 8, 3, 128, 64, 16, 4) == 0
