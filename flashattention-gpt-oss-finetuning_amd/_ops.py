@@ -1,5 +1,9 @@
 """Tensor-level calls into libfa_gfx950.so: argument marshalling, output allocation, streams.
 
+forward() / backward() go through the C++ binding fa_torch (csrc/fa_torch.cpp) when it is
+built, else through the ctypes structures below; FwdCall / BwdCall are prepared ctypes launches
+used to time single kernels.
+
 PyTorch provides device memory (the caching allocator) and the current HIP stream; every
 FLOP runs in the library's HIP kernels.  Inputs the kernels cannot read directly (head-dim
 stride != 1, rows not 16-byte aligned) are first copied to a contiguous layout, as the
@@ -8,6 +12,7 @@ reference benchmark does for dO (benchmark_backward_speed.py:510).
 from __future__ import annotations
 
 import ctypes
+import importlib
 
 import torch
 
@@ -111,8 +116,28 @@ class FwdCall:
         _lib.raise_for_status(rc, "fa_fwd")
 
 
+def _binding():
+    """The C++ binding (csrc/fa_torch.cpp) when it is built, else None.  Both paths call the same
+    C ABI of libfa_gfx950.so; the binding only does the per-call host work in C++."""
+    global _BINDING
+    if _BINDING is False:
+        try:
+            _lib.lib()  # the HIP library is required either way (raises when missing)
+            _BINDING = importlib.import_module(__package__ + ".fa_torch")
+        except ImportError:
+            _BINDING = None
+    return _BINDING
+
+
+_BINDING = False
+
+
 def forward(q, k, v, window: int, sink: int, scale: float):
     """Returns (o, lse) for q [B,Hq,L,D], k/v [B,Hkv,L,D]."""
+    b = _binding()
+    if b is not None:
+        o, lse = b.fwd(q, k, v, int(window), int(sink), float(scale))
+        return o, lse
     call = FwdCall(q, k, v, window, sink, scale)
     call.run()
     return call.o, call.lse
@@ -171,6 +196,10 @@ class BwdCall:
 
 def backward(q, k, v, o, lse, do, window: int, sink: int, scale: float):
     """Returns (dq, dk, dv) in the input dtype."""
+    b = _binding()
+    if b is not None:
+        dq, dk, dv = b.bwd(q, k, v, o, lse, do, int(window), int(sink), float(scale))
+        return dq, dk, dv
     call = BwdCall(q, k, v, o, lse, do, window, sink, scale)
     call.run()
     return call.dq, call.dk, call.dv

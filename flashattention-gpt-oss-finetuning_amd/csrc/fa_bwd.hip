@@ -270,13 +270,15 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   constexpr int TILE = 32 * D;               // 32 rows of Q or dO, swizzled row-major
   constexpr int SLOT = 2 * TILE + 128;       // Q, dO, then lse2[32] and delta[32] as fp32
   constexpr int STAGE = 2 * SLOT;            // two items per step
+  constexpr int NSTG = 3;                    // LDS stages: compute, landed, in flight
   constexpr int CPR = D / 8;                 // 16-byte chunks per row
   constexpr int RED = 2 * 2 * DB * 16 * 64;  // fp32 partials of the two hh = 1 waves
-  constexpr int LDS_ELEMS = (2 * STAGE > 2 * RED) ? 2 * STAGE : 2 * RED;
+  constexpr int LDS_ELEMS = (NSTG * STAGE > 2 * RED) ? NSTG * STAGE : 2 * RED;
   __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hf = lane >> 5;
   const int kh = wave & 1, hh = wave >> 1;
   const int L = a.L, W = a.W, S = a.S, G = a.G;
@@ -339,67 +341,65 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   const int n_steps = G * n_qp;
 
   // ---- staging.  The four 32-row tiles of a step (slot 0 Q, slot 0 dO, slot 1 Q, slot 1 dO)
-  // are loaded through buffer resources spanning one query head's rows [0, L) (rows past L read
-  // as zero; a head slice is < 2^31 bytes, checked by the C ABI).  Descriptors change only with
-  // the head; a step adds its block offset to loop-invariant per-lane offsets.  Load i handles
-  // tile i / ITPT (compile-time) and chunk (i % ITPT) * 256 + tid of it. ------------------------
-  constexpr int TPI = 32 * CPR;                  // 16-byte chunks per tile
-  constexpr int ITPT = TPI >= 256 ? TPI / 256 : 1;
-  constexpr bool ALL_ON = TPI >= 256;            // every thread loads a chunk of every tile
-  constexpr int NL = 4 * ITPT;
-  uint32_t lane_off_q[ITPT], lane_off_d[ITPT];
-  int lane_lds[ITPT];
-  bool lane_on[ITPT];
+  // go straight from HBM into an LDS stage by DMA (buffer_load ... lds): wave w loads tile w,
+  // IPT instructions of 64 lanes x 16 bytes, each writing 1 KiB of the swizzled tile in lane
+  // order -- so lane l of instruction p loads the global chunk that the swizzle places at
+  // 16-byte position 64p + l.  Loads go through buffer resources spanning one query head's rows
+  // [0, L) (rows past L read as zero; a head slice is < 2^31 bytes, checked by the C ABI);
+  // descriptors change only with the head.  The row statistics (lse, delta: one value per
+  // thread of the first two waves) take the register path, transformed on their way to LDS.
+  // Three stages rotate: the step being computed, the next one (landed), and the one after
+  // (in flight), so a step's tiles have two steps of compute to arrive. ------------------------
+  constexpr int IPT = 32 * D * 2 / 1024;         // DMA instructions per tile (1 KiB each)
+  const int t_slot = wave >> 1, t_kind = wave & 1;  // this wave's tile: slot, Q (0) or dO (1)
+  const int64_t t_rs = t_kind ? a.sdo[2] : a.sq[2];  // row stride of the tile's tensor
+  uint32_t dma_off[IPT];
 #pragma unroll
-  for (int i = 0; i < ITPT; ++i) {
-    const int wc = i * 256 + tid;
-    const int row = wc / CPR, col = wc % CPR;
-    lane_on[i] = ALL_ON || wc < TPI;
-    lane_off_q[i] = uint32_t((int64_t(row) * a.sq[2] + 8 * col) * 2);
-    lane_off_d[i] = uint32_t((int64_t(row) * a.sdo[2] + 8 * col) * 2);
-    lane_lds[i] = swz_off<D>(row, 8 * col);
+  for (int p = 0; p < IPT; ++p) {
+    const int pos = 64 * p + lane;             // 16-byte position in the swizzled tile
+    const int row = pos / CPR, phys = pos % CPR;
+    const int col = phys ^ swz<D>(row);        // the logical chunk stored there
+    dma_off[p] = uint32_t((int64_t(row) * t_rs + 8 * col) * 2);
   }
   const char* qslice = reinterpret_cast<const char*>(a.q) + 2 * (int64_t(b) * a.sq[0] + int64_t(kvh) * G * a.sq[1]);
   const char* dslice = reinterpret_cast<const char*>(a.dout) + 2 * (int64_t(b) * a.sdo[0] + int64_t(kvh) * G * a.sdo[1]);
   const char* lslice = reinterpret_cast<const char*>(a.lse + int64_t(b) * a.slse[0] + int64_t(kvh) * G * a.slse[1]);
   const char* tslice = reinterpret_cast<const char*>(a.delta + (int64_t(b) * a.Hq + int64_t(kvh) * G) * a.Lp);
-  const uint32_t nq = span_bytes(L, a.sq[2], D), nd = span_bytes(L, a.sdo[2], D);
+  const char* tile_slice = t_kind ? dslice : qslice;
+  const int64_t t_hs = t_kind ? a.sdo[1] : a.sq[1];  // head stride of the tile's tensor
+  const uint32_t nt_bytes = span_bytes(L, t_rs, D);
   const uint32_t nl = uint32_t((int64_t(L - 1) * a.slse[2] + 1) * 4), nt = uint32_t(L * 4);
   // bytes per 32-row block
-  const uint32_t bq = uint32_t(64 * a.sq[2]), bd = uint32_t(64 * a.sdo[2]), bl = uint32_t(128 * a.slse[2]);
+  const uint32_t bt = uint32_t(64 * t_rs), bl = uint32_t(128 * a.slse[2]);
   // stats: thread tid < 128 loads row tid % 32 of (slot tid / 64, kind (tid / 32) % 2).  Every
   // thread issues both loads (threads >= 128 at an offset past any buffer, which reads 0), so
   // the number of loads in flight is the same on every path.
   const int st_slot = (tid >> 6) & 1, st_kind = (tid >> 5) & 1, st_row = tid & 31;
   const uint32_t st_far = tid < 128 ? 0u : 0x80000000u;
   const uint32_t lse_off = uint32_t(int64_t(st_row) * 4 * a.slse[2]) | st_far, dlt_off = uint32_t(st_row * 4) | st_far;
-  // Register staging of one step; two of them alternate so that a step's loads have two steps
-  // of compute to arrive (issued at step s - 1, stored to LDS at the end of step s).
+  // Register part of a step: the two row statistics and the step's first row.
   struct Stage {
-    u32x4 v[NL];
     float stat, stat2;  // lse, delta
     int q0;             // first row of slot 0
   };
   Stage sa, sb;
   // fetch side: the step (fh, fp) being loaded and the descriptors of head fh
   int fh = 0, fp = 0;
-  rsrc_t rq, rd, rl, rt;
+  rsrc_t rtile, rl, rt;
   auto set_head = [&]() {
-    rq = make_rsrc(qslice + int64_t(fh) * 2 * a.sq[1], nq);
-    rd = make_rsrc(dslice + int64_t(fh) * 2 * a.sdo[1], nd);
+    rtile = make_rsrc(tile_slice + int64_t(fh) * 2 * t_hs, nt_bytes);
     rl = make_rsrc(lslice + int64_t(fh) * 4 * a.slse[1], nl);
     rt = make_rsrc(tslice + int64_t(fh) * 4 * a.Lp, nt);
   };
-  // loads the step (fh, fp) into st and moves the fetch side to the next step
-  auto gload = [&](Stage& st) {
+  // issues the loads of step (fh, fp) -- tiles into LDS stage `buf`, statistics into st -- and
+  // moves the fetch side to the next step
+  auto gload = [&](Stage& st, int buf) {
     const uint32_t qb0 = uint32_t(qb_lo + 2 * fp);  // block of slot 0
+    const uint32_t blk_off = (qb0 + uint32_t(t_slot)) * bt;
+    uint16_t* dst = lds + buf * STAGE + t_slot * SLOT + t_kind * TILE;
 #pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      const int t = i / ITPT, j = i % ITPT;  // compile-time
-      const uint32_t blk = qb0 + uint32_t(t >> 1);
-      if (ALL_ON || lane_on[j])
-        st.v[i] = (t & 1) ? buf_ld16(rd, lane_off_d[j] + blk * bd) : buf_ld16(rq, lane_off_q[j] + blk * bq);
-    }
+    for (int p = 0; p < IPT; ++p)
+      buf_dma16(rtile, dst + 512 * p, dma_off[p] + blk_off);
     // raw values: any arithmetic on them here would make the wave wait for the loads now
     const uint32_t blk = qb0 + uint32_t(st_slot);
     st.stat = buf_ldf(rl, lse_off + blk * bl);
@@ -411,20 +411,25 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
       if (fh < G) set_head();
     }
   };
+  // lse -> lse * log2(e) (+inf for rows past L, which read 0: their P is exactly 0);
+  // delta -> -delta, the initial value of the dP accumulator
   auto sstore = [&](const Stage& st, int buf) {
-    uint16_t* stage = lds + buf * STAGE;
-#pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      const int t = i / ITPT, j = i % ITPT;
-      if (ALL_ON || lane_on[j]) st16(stage + (t >> 1) * SLOT + (t & 1) * TILE + lane_lds[j], st.v[i]);
-    }
-    // lse -> lse * log2(e) (+inf for rows past L, which read 0: their P is exactly 0);
-    // delta -> -delta, the initial value of the dP accumulator
     if (tid < 128) {
       const int qrow = st.q0 + 32 * st_slot + st_row;
       const float v = st_kind ? -st.stat2 : (qrow < L ? st.stat * kLog2e : __builtin_inff());
-      reinterpret_cast<float*>(stage + st_slot * SLOT + 2 * TILE)[st_kind * 32 + st_row] = v;
+      reinterpret_cast<float*>(lds + buf * STAGE + st_slot * SLOT + 2 * TILE)[st_kind * 32 + st_row] = v;
     }
+  };
+  // End of a step: this wave's loads of the next step have landed (the step after may still be
+  // in flight: its IPT DMA instructions and 2 statistics loads), its statistics are stored, and
+  // every wave has passed this point.  Waits and barrier are explicit: the compiler would
+  // otherwise also wait for the step still in flight.
+  auto step_end = [&]() {
+    static_assert(IPT + 2 <= 15, "vmcnt immediate");
+    if constexpr (IPT + 2 == 3) asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (IPT + 2 == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (IPT + 2 == 6) asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   };
 
   // Per-lane constants of the compute.  The mask is one unsigned compare per element:
@@ -436,12 +441,12 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   else lim = key < S ? (partial_block ? unsigned(max(wqhi - key, 0)) : 0x80000000u) : unsigned(W);
   const int mref = is_chunk ? qlo : key;  // mask coordinate: row - mref
 
-  // One item of this wave: the (head, block) pair cp of step `step`, slot hh.
-  auto compute = [&](int step, int cp) {
+  // One item of this wave: the (head, block) pair cp of the step in LDS stage `buf`, slot hh.
+  auto compute = [&](int buf, int cp) {
     const int qbi = 2 * cp + hh;
     const int qr0 = 32 * (qb_lo + qbi);
     if (!(wave_on && qbi < n_qb && qr0 + 32 > wqlo && qr0 < wqhi && kv_half_needs(qr0, ks0, L, W, S))) return;
-    const uint16_t* Qt = lds + (step & 1) * STAGE + hh * SLOT;
+    const uint16_t* Qt = lds + buf * STAGE + hh * SLOT;
     const uint16_t* Dt = Qt + TILE;
     const float* lse2 = reinterpret_cast<const float*>(Qt + 2 * TILE);
     const float* ndlt = lse2 + 32;  // -delta
@@ -496,35 +501,43 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   // Descriptors are built before any load, whatever the number of steps (a workgroup can own
   // no items: a chunk whose rows all lie inside the window).
   set_head();
+  int cb = 0;  // LDS stage of the step being computed; (cb + 1) % 3 holds the next step
   if (n_steps > 0) {
-    gload(sa);
+    gload(sa, 0);  // step 0
+    gload(sb, 1);  // step 1
+    // step 0 landed (step 1 may be in flight)
+    if constexpr (IPT + 2 == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+    else if constexpr (IPT + 2 == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else if constexpr (IPT + 2 == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
     sstore(sa, 0);
-    // Nothing may be outstanding here: the compiler's wait counting is conservative across the
-    // loop's back edge and would otherwise wait for in-flight prefetches before every MFMA.
-    __builtin_amdgcn_s_waitcnt(0);
-    gload(sa);  // step 1
+    step_end();
   }
-  __syncthreads();
-  // Step s computes LDS buffer s & 1, issues the loads of step s + 2 and stores step s + 1
-  // (loaded during step s - 1) into the other buffer.
-  // The loads are issued unconditionally (past the last step they read the last head's rows or
-  // zeros and are never used), so the wait counts before the LDS stores are exact.
+  // Step s computes stage cb, issues the loads of step s + 2 into stage (cb + 2) % 3 (last read
+  // at step s - 1, before the barrier that ended it) and stores the statistics of step s + 1.
+  // Loads past the last step are issued anyway (they read the last head's rows or zeros into a
+  // stage that is never computed), so every step keeps the same number of loads in flight.
   int cp = 0;  // block pair of the step being computed
   for (int step = 0; step < n_steps; step += 2) {
-    gload(sb);
-    compute(step, cp);
+    gload(sa, cb == 0 ? 2 : cb - 1);
+    compute(cb, cp);
     if (++cp == n_qp) cp = 0;
-    if (step + 1 < n_steps) sstore(sa, 1);
-    __syncthreads();
+    cb = cb == 2 ? 0 : cb + 1;
+    sstore(sb, cb);
+    step_end();
     if (step + 1 >= n_steps) break;
-    gload(sa);
-    compute(step + 1, cp);
+    gload(sb, cb == 0 ? 2 : cb - 1);
+    compute(cb, cp);
     if (++cp == n_qp) cp = 0;
-    if (step + 2 < n_steps) sstore(sb, 0);
-    __syncthreads();
+    cb = cb == 2 ? 0 : cb + 1;
+    sstore(sa, cb);
+    step_end();
   }
 
   // ---- add the two head slots' partial sums (hh = 0 gets hh = 1's), fixed order ---------------
+  // The stages are reused: nothing may still be landing in them.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
   float* red = reinterpret_cast<float*>(lds);
   if (hh == 1) {
 #pragma unroll

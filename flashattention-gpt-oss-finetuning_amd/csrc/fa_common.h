@@ -131,6 +131,13 @@ __device__ __forceinline__ u32x4 buf_ld16(rsrc_t r, uint32_t off) {
 __device__ __forceinline__ float buf_ldf(rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
+// LDS DMA (buffer_load_dwordx4 ... lds): every lane loads 16 bytes at byte offset `off` of the
+// buffer, and lane l's bytes land at lds_dst + 16 l (lds_dst is wave-uniform).  Out-of-range
+// offsets land zeros.  Completion is counted by vmcnt like any load; an LDS read of the data
+// must wait for it explicitly (the compiler does not).  (Checked on hardware.)
+__device__ __forceinline__ void buf_dma16(rsrc_t r, uint16_t* lds_dst, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds_dst), 16, off, 0, 0, 0);
+}
 // Bytes spanned by `rows` rows of `cols` 16-bit elements with row stride `stride` (0 if none).
 __device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride, int cols) {
   return rows > 0 ? uint32_t((int64_t(rows - 1) * stride + cols) * 2) : 0u;
