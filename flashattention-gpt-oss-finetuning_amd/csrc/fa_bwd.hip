@@ -27,12 +27,17 @@
 namespace fa {
 
 // ---------------------------------------------------------------------------------------------
-// dQ (query-major).  Per wave: 32 rows x HPW heads.  Per 32-key step, with S^T = K Q^T and
-// dP^T = V dO^T in C layout (lane = query row), P and dS are per-lane elementwise, and
-// dQ^T += K^T dS^T takes dS^T straight from registers while K^T is read transposed from the
-// row-major K block in LDS.
+// dQ (query-major), persistent.  A tile is 32*wq rows x wh query heads of one KV group; a wave
+// owns 32 rows of one head.  Per 32-key step, with S^T = K Q^T and dP^T = V dO^T in C layout
+// (lane = query row), P and dS are per-lane elementwise, and dQ^T += K^T dS^T takes dS^T straight
+// from registers while K^T is read transposed from the row-major K block in LDS.
+//
+// The grid is one wave of workgroups (resident together); every XCD owns a contiguous range of
+// tiles (neighbouring tiles share K/V rows in that XCD's L2) and its workgroups walk it with the
+// XCD's workgroup count as stride.  The rows of a workgroup's next tile (Q, dO, O, lse) are
+// loaded while the current tile computes, so the row traffic overlaps the MFMA work.
 // ---------------------------------------------------------------------------------------------
-template <typename E, int D, int HPW>
+template <typename E, int D>
 __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
   constexpr int BN = 64;
   constexpr int KS = D / 16;
@@ -41,77 +46,66 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
   constexpr int CPB = BN * D / 8;          // 16-byte chunks per 64-key block of K (or V)
   constexpr int NK = (CPB + 255) / 256;    // chunks per thread
   constexpr bool ALL_ON = CPB >= 256;      // every thread loads a chunk of every tile
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF];
+  constexpr int NX = 8;                    // XCDs: workgroup i runs on XCD i % 8
+  constexpr int STASH = 3 * KS * 512;      // per wave: the next tile's Q, dO, O fragments
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF + 4 * STASH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int r32 = lane & 31, hf = lane >> 5;
-
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int qt = tile % a.n_qtiles;
-  const int hg = tile / a.n_qtiles;
-  const int hwg = HPW * a.wh;
-  const int groups_per_batch = a.Hq / hwg;
-  const int b = hg / groups_per_batch;
-  const int h0 = (hg % groups_per_batch) * hwg;
-  const int kvh = h0 / a.G;
-  const int BM = 32 * a.wq;
-  const int q0 = qt * BM;
-  const int qw = q0 + 32 * (wave % a.wq);
-  const int hw = h0 + HPW * (wave / a.wq);
-  const int q = qw + r32;
-  const bool wave_active = qw < a.L;
   const int L = a.L, W = a.W, S = a.S;
 
-  // Row operands and row statistics.  delta = rowsum(dO o O) is stored for the dK/dV kernel;
-  // the dP accumulator of every key tile starts from -delta, so dS = P * acc.
-  u32x4 qf[HPW][KS], dof[HPW][KS];
-  float lse2[HPW], ndelta[HPW];
-#pragma unroll
-  for (int h = 0; h < HPW; ++h) {
-    const char* qp = reinterpret_cast<const char*>(a.q) +
-                     2 * (int64_t(b) * a.sq[0] + int64_t(hw + h) * a.sq[1] + int64_t(q) * a.sq[2]);
-    const char* dop = reinterpret_cast<const char*>(a.dout) +
-                      2 * (int64_t(b) * a.sdo[0] + int64_t(hw + h) * a.sdo[1] + int64_t(q) * a.sdo[2]);
-    const char* op = reinterpret_cast<const char*>(a.o) +
-                     2 * (int64_t(b) * a.so[0] + int64_t(hw + h) * a.so[1] + int64_t(q) * a.so[2]);
-    float dsum = 0.f;
+  // this workgroup's tiles: its XCD's range [t_lo, t_hi), from pos with stride wgs_x
+  const int groups = a.B * a.Hq / a.wh;
+  const int n_tiles = a.n_qtiles * groups;
+  const int xcd = blockIdx.x % NX, pos = blockIdx.x / NX, wgs_x = gridDim.x / NX;
+  const int per = n_tiles / NX, rem = n_tiles % NX;
+  const int t_lo = xcd * per + min(xcd, rem), t_hi = t_lo + per + (xcd < rem ? 1 : 0);
+
+  // tile -> (b, KV head, this wave's head hw, first row qw)
+  struct TileIdx {
+    int b, kvh, hw, q0, qw;
+  };
+  auto decode = [&](int tile) {
+    TileIdx t;
+    const int qt = tile % a.n_qtiles, hg = tile / a.n_qtiles;
+    const int groups_per_batch = a.Hq / a.wh;
+    t.b = hg / groups_per_batch;
+    const int h0 = (hg % groups_per_batch) * a.wh;
+    t.kvh = h0 / a.G;
+    t.q0 = qt * 32 * a.wq;
+    t.qw = t.q0 + 32 * (wave % a.wq);
+    t.hw = h0 + wave / a.wq;
+    return t;
+  };
+
+  // The rows of a tile for this wave: Q, dO and O fragments (lane = row, head-dim slice
+  // [hf*D/2 + 8ks, +8)) go by LDS DMA into the wave's own stash -- fragment (tensor x, ks) of
+  // lane l at 16 bytes each, in lane order -- so they occupy no registers while the current
+  // tile computes; the row's lse goes to a register.  Buffer resources over the head's rows
+  // [0, L): rows past L read as zero.
+  uint16_t* stash = lds + 2 * BUF + wave * STASH;
+  const uint32_t nq = span_bytes(L, a.sq[2], D), nd = span_bytes(L, a.sdo[2], D), no = span_bytes(L, a.so[2], D);
+  const uint32_t nl = uint32_t((int64_t(L - 1) * a.slse[2] + 1) * 4);
+  auto stash_rows = [&](const TileIdx& t) {
+    const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(a.q) + 2 * (int64_t(t.b) * a.sq[0] + int64_t(t.hw) * a.sq[1]), nq);
+    const rsrc_t rd = make_rsrc(reinterpret_cast<const char*>(a.dout) + 2 * (int64_t(t.b) * a.sdo[0] + int64_t(t.hw) * a.sdo[1]), nd);
+    const rsrc_t ro = make_rsrc(reinterpret_cast<const char*>(a.o) + 2 * (int64_t(t.b) * a.so[0] + int64_t(t.hw) * a.so[1]), no);
+    const int q = t.qw + r32;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int d = hf * (D / 2) + 8 * ks;
-      u32x4 qv = zero16(), dv = zero16(), ov = zero16();
-      if (q < L) {
-        qv = ld16(qp + 2 * d);
-        dv = ld16(dop + 2 * d);
-        ov = ld16(op + 2 * d);
-      }
-      qf[h][ks] = qv ^ a.qsign;
-      dof[h][ks] = dv;
-      dsum += dot8<E>(dv, ov);
+      buf_dma16(rq, stash + (0 * KS + ks) * 512, uint32_t((int64_t(q) * a.sq[2] + d) * 2));
+      buf_dma16(rd, stash + (1 * KS + ks) * 512, uint32_t((int64_t(q) * a.sdo[2] + d) * 2));
+      buf_dma16(ro, stash + (2 * KS + ks) * 512, uint32_t((int64_t(q) * a.so[2] + d) * 2));
     }
-    const float delta = sum_halves(dsum);
-    ndelta[h] = -delta;
-    lse2[h] = __builtin_inff();
-    if (q < L) {
-      lse2[h] = a.lse[int64_t(b) * a.slse[0] + int64_t(hw + h) * a.slse[1] + int64_t(q) * a.slse[2]] * kLog2e;
-      if (hf == 0) a.delta[(int64_t(b) * a.Hq + hw + h) * a.Lp + q] = delta;
-    }
-  }
+  };
+  auto load_lse = [&](const TileIdx& t) {
+    const rsrc_t rl = make_rsrc(a.lse + int64_t(t.b) * a.slse[0] + int64_t(t.hw) * a.slse[1], nl);
+    return buf_ldf(rl, uint32_t(int64_t(t.qw + r32) * a.slse[2] * 4));
+  };
 
-  f32x16 acc[HPW][DB];
-#pragma unroll
-  for (int h = 0; h < HPW; ++h)
-#pragma unroll
-    for (int db = 0; db < DB; ++db) acc[h][db] = f32x16{};
-
-  const QPlan plan = qplan(q0, BM, L, W, S);
-
-  // K/V of the KV head through buffer resources spanning rows [0, L): rows past L read as zero
-  // (a slice is < 2^31 bytes, checked by the C ABI).
-  const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * (int64_t(b) * a.sk[0] + int64_t(kvh) * a.sk[1]),
-                              span_bytes(L, a.sk[2], D));
-  const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * (int64_t(b) * a.sv[0] + int64_t(kvh) * a.sv[1]),
-                              span_bytes(L, a.sv[2], D));
+  // K/V staging offsets (the same for every tile)
   uint32_t off_k[NK], off_v[NK];
   int off_l[NK];
 #pragma unroll
@@ -123,128 +117,162 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
     off_l[it] = swz_off<D>(row, 8 * col);
   }
   const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
+  const uint32_t nk_bytes = span_bytes(L, a.sk[2], D), nv_bytes = span_bytes(L, a.sv[2], D);
 
-  u32x4 kreg[NK], vreg[NK];
-  auto gload = [&](int kb) {
+  int tile = t_lo + pos;
+  float lse_next = 0.f;
+  if (tile < t_hi) {
+    const TileIdx t0 = decode(tile);
+    stash_rows(t0);
+    lse_next = load_lse(t0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  for (; tile < t_hi; tile += wgs_x) {
+    const TileIdx t = decode(tile);
+    const int qw = t.qw, q = qw + r32;
+    const bool wave_active = qw < L;
+
+    // Row operands and row statistics, from the stash (this wave's own DMA, complete by now:
+    // see the wait after the key loop).  delta = rowsum(dO o O) is stored for the dK/dV kernel;
+    // the dP accumulator of every key tile starts from -delta, so dS = P * acc.
+    u32x4 qf[KS], dof[KS];
+    float dsum = 0.f;
 #pragma unroll
-    for (int it = 0; it < NK; ++it) {
-      if (ALL_ON || tid + 256 * it < CPB) {
-        kreg[it] = buf_ld16(rk, off_k[it] + uint32_t(kb) * bk);
-        vreg[it] = buf_ld16(rv, off_v[it] + uint32_t(kb) * bv);
-      }
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[ks] = lds16(stash + (0 * KS + ks) * 512 + 8 * lane) ^ a.qsign;
+      dof[ks] = lds16(stash + (1 * KS + ks) * 512 + 8 * lane);
+      dsum += dot8<E>(dof[ks], lds16(stash + (2 * KS + ks) * 512 + 8 * lane));
     }
-  };
-  auto sstore = [&](int buf) {
-    uint16_t* Kl = lds + buf * BUF;
-    uint16_t* Vl = Kl + BN * D;
-#pragma unroll
-    for (int it = 0; it < NK; ++it) {
-      if (ALL_ON || tid + 256 * it < CPB) {
-        st16(Kl + off_l[it], kreg[it]);
-        st16(Vl + off_l[it], vreg[it]);
-      }
-    }
-  };
+    const float delta = sum_halves(dsum);
+    const float ndelta = -delta;
+    const float lse2 = q < L ? lse_next * kLog2e : __builtin_inff();
+    if (q < L && hf == 0) a.delta[(int64_t(t.b) * a.Hq + t.hw) * a.Lp + q] = delta;
 
-  gload(qplan_block(plan, 0));
-  sstore(0);
-  __syncthreads();
+    f32x16 acc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
 
-  for (int i = 0; i < plan.nb; ++i) {
-    const int kb = qplan_block(plan, i);
-    const bool more = i + 1 < plan.nb;
-    if (more) gload(qplan_block(plan, i + 1));
-    if (wave_active) {
-      const uint16_t* Kl = lds + (i & 1) * BUF;
-      const uint16_t* Vl = Kl + BN * D;
+    const QPlan plan = qplan(t.q0, 32 * a.wq, L, W, S);
+    const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * (int64_t(t.b) * a.sk[0] + int64_t(t.kvh) * a.sk[1]), nk_bytes);
+    const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * (int64_t(t.b) * a.sv[0] + int64_t(t.kvh) * a.sv[1]), nv_bytes);
+    u32x4 kreg[NK], vreg[NK];
+    auto gload = [&](int kb) {
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        const int ks0 = kb + 32 * sb;
-        if (!wave_needs(ks0, qw, L, W, S)) continue;
-        // S^T = K Q^T and dP^T - delta = V dO^T - delta for every head (K/V fragments shared).
-        // Masked tiles start S^T from an additive bias, 0 (allowed) or -inf (masked), so P is
-        // exactly 0 there; the test is the forward's: register e holds key ks0 + 4hf + off(e),
-        // allowed = (dq0 - off) < lim.
-        u32x4 kf[KS], vf[KS];
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const int off = swz_off<D>(32 * sb + r32, hf * (D / 2) + 8 * ks);
-          kf[ks] = *reinterpret_cast<const u32x4*>(Kl + off);
-          vf[ks] = *reinterpret_cast<const u32x4*>(Vl + off);
+      for (int it = 0; it < NK; ++it) {
+        if (ALL_ON || tid + 256 * it < CPB) {
+          kreg[it] = buf_ld16(rk, off_k[it] + uint32_t(kb) * bk);
+          vreg[it] = buf_ld16(rv, off_v[it] + uint32_t(kb) * bv);
         }
-        f32x16 s[HPW], dp[HPW];
-        auto qk = [&](const f32x16& c0) {
+      }
+    };
+    auto sstore = [&](int buf) {
+      uint16_t* Kl = lds + buf * BUF;
+      uint16_t* Vl = Kl + BN * D;
 #pragma unroll
-          for (int h = 0; h < HPW; ++h) {
+      for (int it = 0; it < NK; ++it) {
+        if (ALL_ON || tid + 256 * it < CPB) {
+          st16(Kl + off_l[it], kreg[it]);
+          st16(Vl + off_l[it], vreg[it]);
+        }
+      }
+    };
+
+    gload(qplan_block(plan, 0));
+    sstore(0);
+    __syncthreads();
+
+    for (int i = 0; i < plan.nb; ++i) {
+      const int kb = qplan_block(plan, i);
+      const bool more = i + 1 < plan.nb;
+      if (more) gload(qplan_block(plan, i + 1));
+      // the next tile's rows into the stash, once this tile's have been read out of it
+      if (i == 0 && tile + wgs_x < t_hi) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const TileIdx tn = decode(tile + wgs_x);
+        stash_rows(tn);
+        lse_next = load_lse(tn);
+      }
+      if (wave_active) {
+        const uint16_t* Kl = lds + (i & 1) * BUF;
+        const uint16_t* Vl = Kl + BN * D;
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+          const int ks0 = kb + 32 * sb;
+          if (!wave_needs(ks0, qw, L, W, S)) continue;
+          // S^T = K Q^T and dP^T - delta = V dO^T - delta.  Masked tiles start S^T from an
+          // additive bias, 0 (allowed) or -inf (masked), so P is exactly 0 there; the test is
+          // the forward's: register e holds key ks0 + 4hf + off(e), allowed = (dq0 - off) < lim.
+          u32x4 kf[KS], vf[KS];
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            const int off = swz_off<D>(32 * sb + r32, hf * (D / 2) + 8 * ks);
+            kf[ks] = *reinterpret_cast<const u32x4*>(Kl + off);
+            vf[ks] = *reinterpret_cast<const u32x4*>(Vl + off);
+          }
+          f32x16 s, dp;
+          auto qk = [&](const f32x16& c0) {
             f32x16 d0;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) d0[e] = ndelta[h];
+            for (int e = 0; e < 16; ++e) d0[e] = ndelta;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-              s[h] = E::mfma(kf[ks], qf[h][ks], ks == 0 ? c0 : s[h]);
-              dp[h] = E::mfma(vf[ks], dof[h][ks], ks == 0 ? d0 : dp[h]);
+              s = E::mfma(kf[ks], qf[ks], ks == 0 ? c0 : s);
+              dp = E::mfma(vf[ks], dof[ks], ks == 0 ? d0 : dp);
             }
-          }
-        };
-        if (tile_full(ks0, qw, W, S)) {
-          qk(f32x16{});
-        } else {
-          f32x16 bias;
-          const int dq0 = q - ks0 - 4 * hf;
-          if (ks0 >= S || ks0 + 32 <= S) {  // one limit for all 32 keys
-            const unsigned lim = ks0 >= S ? unsigned(W) : 0x80000000u;
+          };
+          if (tile_full(ks0, qw, W, S)) {
+            qk(f32x16{});
+          } else {
+            f32x16 bias;
+            const int dq0 = q - ks0 - 4 * hf;
+            if (ks0 >= S || ks0 + 32 <= S) {  // one limit for all 32 keys
+              const unsigned lim = ks0 >= S ? unsigned(W) : 0x80000000u;
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-              bias[e] = unsigned(dq0 - (8 * (e / 4) + (e % 4))) < lim ? 0.f : kNegInf;
-          } else {  // the sink boundary S falls inside these keys
-            const int sl = S - ks0 - 4 * hf;  // keys with off < sl are sinks
+              for (int e = 0; e < 16; ++e)
+                bias[e] = unsigned(dq0 - (8 * (e / 4) + (e % 4))) < lim ? 0.f : kNegInf;
+            } else {  // the sink boundary S falls inside these keys
+              const int sl = S - ks0 - 4 * hf;  // keys with off < sl are sinks
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              const int off = 8 * (e / 4) + (e % 4);
-              bias[e] = unsigned(dq0 - off) < (off < sl ? 0x80000000u : unsigned(W)) ? 0.f : kNegInf;
+              for (int e = 0; e < 16; ++e) {
+                const int off = 8 * (e / 4) + (e % 4);
+                bias[e] = unsigned(dq0 - off) < (off < sl ? 0x80000000u : unsigned(W)) ? 0.f : kNegInf;
+              }
             }
+            qk(bias);
           }
-          qk(bias);
-        }
-        // K^T operands of dQ^T += K^T dS^T, shared by the heads: read transposed from the
-        // row-major K block, keys in the row order of the dS^T C tile.
-        u32x4 kt[DB][2];
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int t = 0; t < 2; ++t) kt[db][t] = tr_frag_swz<D>(Kl, 32 * sb + 16 * t, 32 * db, D);
-#pragma unroll
-        for (int h = 0; h < HPW; ++h) {
+          // dQ^T += K^T dS^T: K^T read transposed from the row-major K block, keys in the row
+          // order of the dS^T C tile
           float ds[16];
 #pragma unroll
-          for (int e = 0; e < 16; ++e) ds[e] = fast_exp2(fmaf(s[h][e], a.c, -lse2[h])) * dp[h][e];
+          for (int e = 0; e < 16; ++e) ds[e] = fast_exp2(fmaf(s[e], a.c, -lse2)) * dp[e];
           const u32x4 d0 = pack8<E>(ds), d1 = pack8<E>(ds + 8);
 #pragma unroll
           for (int db = 0; db < DB; ++db) {
-            acc[h][db] = E::mfma(kt[db][0], d0, acc[h][db]);
-            acc[h][db] = E::mfma(kt[db][1], d1, acc[h][db]);
+            acc[db] = E::mfma(tr_frag_swz<D>(Kl, 32 * sb, 32 * db, D), d0, acc[db]);
+            acc[db] = E::mfma(tr_frag_swz<D>(Kl, 32 * sb + 16, 32 * db, D), d1, acc[db]);
           }
         }
       }
+      if (more) sstore((i + 1) & 1);
+      __syncthreads();
     }
-    if (more) sstore((i + 1) & 1);
-    __syncthreads();
-  }
+    // the next tile's stash has landed (waited here, before this tile's dQ stores, which would
+    // otherwise also be waited for)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  if (!wave_active || q >= L) return;
+    if (wave_active && q < L) {
+      char* dqp = reinterpret_cast<char*>(a.dq) +
+                  2 * (int64_t(t.b) * a.sdq[0] + int64_t(t.hw) * a.sdq[1] + int64_t(q) * a.sdq[2]);
 #pragma unroll
-  for (int h = 0; h < HPW; ++h) {
-    char* dqp = reinterpret_cast<char*>(a.dq) +
-                2 * (int64_t(b) * a.sdq[0] + int64_t(hw + h) * a.sdq[1] + int64_t(q) * a.sdq[2]);
+      for (int db = 0; db < DB; ++db) {
+        if (D == 16 && hf == 1) continue;
+        float v[16];
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      if (D == 16 && hf == 1) continue;
-      float v[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) v[e] = acc[h][db][e] * a.scale;
-      const int d0 = 32 * db + (D >= 32 ? 16 * hf : 0);
-      st16(dqp + 2 * d0, pack8<E>(v));
-      st16(dqp + 2 * (d0 + 8), pack8<E>(v + 8));
+        for (int e = 0; e < 16; ++e) v[e] = acc[db][e] * a.scale;
+        const int d0 = 32 * db + (D >= 32 ? 16 * hf : 0);
+        st16(dqp + 2 * d0, pack8<E>(v));
+        st16(dqp + 2 * (d0 + 8), pack8<E>(v + 8));
+      }
     }
   }
 }
@@ -650,12 +678,34 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Resident workgroups per CU of a kernel (hipOccupancyMaxActiveBlocksPerMultiprocessor,
+// 256 threads), remembered per kernel: it depends only on the kernel's resources.
+template <typename K>
+static int resident_per_cu(K kernel) {
+  static int cached = 0;  // benign race: every thread computes the same value
+  if (cached == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 256, 0) != hipSuccess || n < 1) n = 1;
+    cached = n;
+  }
+  return cached;
+}
+
+static int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n < 1)
+    n = 256;
+  return n;
+}
+
 template <typename E, int D>
-static hipError_t launch_dq_d(const Args& a, int hpw, hipStream_t stream) {
-  const int groups = a.B * a.Hq / (hpw * a.wh);
-  const dim3 grid(a.n_qtiles * groups), block(256);
-  if (hpw == 2) hipLaunchKernelGGL((bwd_dq_kernel<E, D, 2>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((bwd_dq_kernel<E, D, 1>), grid, block, 0, stream, a);
+static hipError_t launch_dq_d(const Args& a, int, hipStream_t stream) {
+  const int n_tiles = a.n_qtiles * (a.B * a.Hq / a.wh);
+  // one resident wave of workgroups, a multiple of the 8 XCDs
+  const int slots = resident_per_cu(bwd_dq_kernel<E, D>) * device_cus();
+  const int wgs = 8 * ((min(n_tiles, slots) + 7) / 8);
+  hipLaunchKernelGGL((bwd_dq_kernel<E, D>), dim3(wgs), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
