@@ -631,36 +631,36 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Sink fold: the dK/dV rows of the chunked sink keys are the sum, in slot order, of the fp32
-// partials that the dK/dV kernel's regular and chunk workgroups wrote for them.  A separate
-// launch, so the partials of every workgroup are visible without a device-wide fence inside the
-// dK/dV kernel.  One thread per (b, KV head, sink key, head-dim index); only keys < S of the
-// chunked blocks exist here.
+// Sink fold: the dK/dV rows of the chunked sink keys are the sum of the fp32 partials that the
+// dK/dV kernel's regular and chunk workgroups wrote for them.  A separate launch, so the
+// partials of every workgroup are visible without a device-wide fence inside the dK/dV kernel.
+// One workgroup per (b, KV head, sink key): thread (g, d) adds slots g, g + NG, g + 2 NG, ...
+// (their loads in flight together), then the NG group sums are added in order g = 0, 1, ... --
+// a fixed order, so results are deterministic.
 // ---------------------------------------------------------------------------------------------
 template <typename E, int D>
 __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
-  const int nrows = min(a.S, kKvKeys * a.nsp);  // sink keys of the chunked blocks
-  const int64_t n = int64_t(a.B) * a.Hkv * nrows * D;
-  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= n) return;
-  const int d = int(i % D);
-  const int key = int((i / D) % nrows);
-  const int64_t bh = i / (int64_t(nrows) * D);  // b * Hkv + kvh
-  const int kvh = int(bh % a.Hkv), b = int(bh / a.Hkv);
-  const int kblk = key / kKvKeys, row = key % kKvKeys;
-  const int64_t blk = bh * a.nsp + kblk;
-  const float* src = a.partial + blk * (a.n_chunks + 1) * 2 * a.srows * D + row * D + d;
-  // Slots are added in order; the loads of up to kBatch slots are in flight together.
+  constexpr int NG = 256 / D;  // slot groups
   constexpr int kBatch = 16;
-  const int64_t kSlot = int64_t(2) * a.srows * D;
+  __shared__ float part[2][NG][D];
+  const int nrows = min(a.S, kKvKeys * a.nsp);  // sink keys of the chunked blocks
+  const int key = blockIdx.x % nrows;
+  const int bh = blockIdx.x / nrows;  // b * Hkv + kvh
+  const int kvh = bh % a.Hkv, b = bh / a.Hkv;
+  const int kblk = key / kKvKeys, row = key % kKvKeys;
+  const int d = threadIdx.x % D, g = threadIdx.x / D;
+  const int64_t blk = int64_t(bh) * a.nsp + kblk;
+  const int64_t slot_stride = int64_t(2) * a.srows * D;
+  const float* src = a.partial + blk * (a.n_chunks + 1) * slot_stride + row * D + d;
   const int ns = a.n_chunks + 1;
   float sk = 0.f, sv = 0.f;
-  for (int s0 = 0; s0 < ns; s0 += kBatch) {
+  for (int s0 = g; s0 < ns; s0 += NG * kBatch) {
     float xk[kBatch], xv[kBatch];
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
-      const bool in = s0 + j < ns;
-      const float* p = src + int64_t(in ? s0 + j : 0) * kSlot;
+      const int sl = s0 + j * NG;
+      const bool in = sl < ns;
+      const float* p = src + int64_t(in ? sl : 0) * slot_stride;
       xk[j] = in ? p[0] : 0.f;
       xv[j] = in ? p[a.srows * D] : 0.f;
     }
@@ -670,14 +670,23 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
       sv += xv[j];
     }
   }
-  const uint32_t pk = E::pack2(sk * a.scale, sv);
+  part[0][g][d] = sk;
+  part[1][g][d] = sv;
+  __syncthreads();
+  if (g != 0) return;
+  float tk = 0.f, tv = 0.f;
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+    tk += part[0][j][d];
+    tv += part[1][j][d];
+  }
+  const uint32_t pk = E::pack2(tk * a.scale, tv);
   reinterpret_cast<uint16_t*>(a.dk)[int64_t(b) * a.sdk[0] + int64_t(kvh) * a.sdk[1] + int64_t(key) * a.sdk[2] + d] =
       uint16_t(pk);
   reinterpret_cast<uint16_t*>(a.dv)[int64_t(b) * a.sdv[0] + int64_t(kvh) * a.sdv[1] + int64_t(key) * a.sdv[2] + d] =
       uint16_t(pk >> 16);
 }
 
-// ---------------------------------------------------------------------------------------------
 // Resident workgroups per CU of a kernel (hipOccupancyMaxActiveBlocksPerMultiprocessor,
 // 256 threads), remembered per kernel: it depends only on the kernel's resources.
 template <typename K>
@@ -715,8 +724,8 @@ static hipError_t launch_dkdv_d(const Args& a, hipStream_t stream) {
   hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), grid, block, 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.nsp == 0) return e;
-  const int64_t n = int64_t(a.B) * a.Hkv * min(a.S, kKvKeys * a.nsp) * D;
-  hipLaunchKernelGGL((bwd_sink_fold_kernel<E, D>), dim3(unsigned((n + 255) / 256)), block, 0, stream, a);
+  const int64_t n = int64_t(a.B) * a.Hkv * min(a.S, kKvKeys * a.nsp);  // one workgroup per sink key
+  hipLaunchKernelGGL((bwd_sink_fold_kernel<E, D>), dim3(unsigned(n)), block, 0, stream, a);
   return hipGetLastError();
 }
 
