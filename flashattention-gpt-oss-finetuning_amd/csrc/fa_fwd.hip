@@ -4,8 +4,11 @@
 // benchmark's _forward_kernel (benchmark_backward_speed.py:146-217).  Same mathematics (FA-2
 // online softmax in the log2 domain), a different decomposition:
 //
-//  * A workgroup is 4 waves covering 32*wq query rows of HPW*wh query heads of ONE KV group,
-//    so every K/V tile staged in LDS serves all of those heads.
+//  * A tile is 32*wq query rows of HPW*wh query heads of ONE KV group, so every K/V block
+//    staged in LDS serves all of those heads.  The grid is one resident wave of 4-wave
+//    workgroups; every XCD owns a contiguous range of tiles (neighbouring tiles share K/V rows in
+//    its L2) and its workgroups walk it, each loading its next tile's Q rows by LDS DMA while the
+//    current tile computes.
 //  * Each wave owns 32 query rows x HPW heads and computes the transposed score tile
 //    S^T = K Q^T (keys x queries) on v_mfma_f32_32x32x16: the lane that holds column q of S^T
 //    owns query row q, so the row max / row sum / rescale of the online softmax are per-lane
@@ -32,40 +35,98 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   constexpr int CPB = BN * D / 8;          // 16-byte chunks per 64-key block of K (or V)
   constexpr int NK = (CPB + 255) / 256;    // chunks per thread
   constexpr bool ALL_ON = CPB >= 256;      // every thread loads a chunk of every tile
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF];
+  constexpr int NX = 8;                    // XCDs: workgroup i runs on XCD i % 8
+  // D = 128 reads Q straight into registers: a stash would take LDS that a second resident
+  // workgroup per CU needs.
+  constexpr bool kStash = D <= 64;
+  constexpr int STASH = kStash ? HPW * KS * 512 : 0;  // per wave: the next tile's Q fragments
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF + 4 * STASH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int r32 = lane & 31, hf = lane >> 5;
-
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int qt = tile % a.n_qtiles;
-  const int hg = tile / a.n_qtiles;
-  const int hwg = HPW * a.wh;
-  const int groups_per_batch = a.Hq / hwg;
-  const int b = hg / groups_per_batch;
-  const int h0 = (hg % groups_per_batch) * hwg;
-  const int kvh = h0 / a.G;
-  const int BM = 32 * a.wq;
-  const int q0 = qt * BM;
-  const int qw = q0 + 32 * (wave % a.wq);
-  const int hw = h0 + HPW * (wave / a.wq);
-  const int q = qw + r32;
-  const bool wave_active = qw < a.L;
   const int L = a.L, W = a.W, S = a.S;
 
-  // Q^T operand fragments: lane (q, hf) holds head-dim slice [hf*D/2 + 8ks, +8) in step ks.
+  // this workgroup's tiles: its XCD's contiguous range [t_lo, t_hi), from pos with stride
+  // wgs_x (neighbouring tiles share K/V rows in that XCD's L2)
+  const int hwg = HPW * a.wh;
+  const int groups_per_batch = a.Hq / hwg;
+  const int n_tiles = a.n_qtiles * a.B * groups_per_batch;
+  const int xcd = blockIdx.x % NX, pos = blockIdx.x / NX, wgs_x = gridDim.x / NX;
+  const int per = n_tiles / NX, rem = n_tiles % NX;
+  const int t_lo = xcd * per + min(xcd, rem), t_hi = t_lo + per + (xcd < rem ? 1 : 0);
+
+  // tile -> (b, KV head, this wave's first head hw, first row of the tile q0 and of the wave qw)
+  struct TileIdx {
+    int b, kvh, hw, q0, qw;
+  };
+  auto decode = [&](int tile) {
+    TileIdx t;
+    const int qt = tile % a.n_qtiles, hg = tile / a.n_qtiles;
+    t.b = hg / groups_per_batch;
+    const int h0 = (hg % groups_per_batch) * hwg;
+    t.kvh = h0 / a.G;
+    t.q0 = qt * 32 * a.wq;
+    t.qw = t.q0 + 32 * (wave % a.wq);
+    t.hw = h0 + HPW * (wave / a.wq);
+    return t;
+  };
+
+  // A tile's Q rows for this wave go by LDS DMA into the wave's own stash -- fragment (h, ks)
+  // of lane l at 16 bytes each, in lane order -- so they occupy no registers while the current
+  // tile computes.  Buffer resources over the head's rows [0, L): rows past L read as zero.
+  uint16_t* stash = lds + 2 * BUF + wave * STASH;
+  const uint32_t nq = span_bytes(L, a.sq[2], D);
+  auto q_rsrc = [&](const TileIdx& t, int h) {
+    return make_rsrc(reinterpret_cast<const char*>(a.q) + 2 * (int64_t(t.b) * a.sq[0] + int64_t(t.hw + h) * a.sq[1]), nq);
+  };
+  auto q_off = [&](const TileIdx& t, int ks) {
+    return uint32_t((int64_t(t.qw + r32) * a.sq[2] + hf * (D / 2) + 8 * ks) * 2);
+  };
+  auto stash_rows = [&](const TileIdx& t) {
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) {
+      const rsrc_t rq = q_rsrc(t, h);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) buf_dma16(rq, stash + (h * KS + ks) * 512, q_off(t, ks));
+    }
+  };
+
+  // K/V staging offsets of the thread's first chunk (the same for every tile); chunk it lies
+  // RSTEP rows further, which keeps the swizzle (it depends on the row mod 8 only).
+  constexpr int RSTEP = 256 / (D / 8);
+  const int row0 = tid / (D / 8), col0 = tid % (D / 8);
+  const uint32_t off_k0 = uint32_t((int64_t(row0) * a.sk[2] + 8 * col0) * 2);
+  const uint32_t off_v0 = uint32_t((int64_t(row0) * a.sv[2] + 8 * col0) * 2);
+  const int off_l0 = swz_off<D>(row0, 8 * col0);
+  const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
+  const uint32_t nk_bytes = span_bytes(L, a.sk[2], D), nv_bytes = span_bytes(L, a.sv[2], D);
+
+  int tile = t_lo + pos;
+  if (kStash && tile < t_hi) {
+    stash_rows(decode(tile));
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  for (; tile < t_hi; tile += wgs_x) {
+  const TileIdx t = decode(tile);
+  const int b = t.b, kvh = t.kvh, hw = t.hw, q0 = t.q0, qw = t.qw;
+  const int BM = 32 * a.wq;
+  const int q = qw + r32;
+  const bool wave_active = qw < L;
+
+  // Q^T operand fragments, from the stash (this wave's own DMA, complete by now: see the wait
+  // after the key loop) or from memory: lane (q, hf) holds head-dim slice [hf*D/2 + 8ks, +8) in
+  // step ks.
   u32x4 qf[HPW][KS];
 #pragma unroll
   for (int h = 0; h < HPW; ++h) {
-    const char* qp = reinterpret_cast<const char*>(a.q) +
-                     2 * (int64_t(b) * a.sq[0] + int64_t(hw + h) * a.sq[1] + int64_t(q) * a.sq[2]);
+    if constexpr (kStash) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      u32x4 v = zero16();
-      if (q < L) v = ld16(qp + 2 * (hf * (D / 2) + 8 * ks));
-      v ^= a.qsign;
-      qf[h][ks] = v;
+      for (int ks = 0; ks < KS; ++ks) qf[h][ks] = lds16(stash + (h * KS + ks) * 512 + 8 * lane) ^ a.qsign;
+    } else {
+      const rsrc_t rq = q_rsrc(t, h);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qf[h][ks] = buf_ld16(rq, q_off(t, ks)) ^ a.qsign;
     }
   }
 
@@ -85,21 +146,9 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // K/V of the KV head through buffer resources spanning rows [0, L): rows past L read as zero,
   // so the loads need no branches (a slice is < 2^31 bytes, checked by the C ABI).
   const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * (int64_t(b) * a.sk[0] + int64_t(kvh) * a.sk[1]),
-                              span_bytes(L, a.sk[2], D));
+                              nk_bytes);
   const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * (int64_t(b) * a.sv[0] + int64_t(kvh) * a.sv[1]),
-                              span_bytes(L, a.sv[2], D));
-  // chunk it of this thread: row c / (D/8), 8 elements from column 8 (c % (D/8)), c = tid + 256 it
-  uint32_t off_k[NK], off_v[NK];
-  int off_l[NK];
-#pragma unroll
-  for (int it = 0; it < NK; ++it) {
-    const int c = tid + 256 * it;
-    const int row = c / (D / 8), col = c % (D / 8);
-    off_k[it] = uint32_t((int64_t(row) * a.sk[2] + 8 * col) * 2);
-    off_v[it] = uint32_t((int64_t(row) * a.sv[2] + 8 * col) * 2);
-    off_l[it] = swz_off<D>(row, 8 * col);
-  }
-  const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
+                              nv_bytes);
 
   // Register staging of the next LDS block.
   u32x4 kreg[NK], vreg[NK];
@@ -107,8 +156,8 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
 #pragma unroll
     for (int it = 0; it < NK; ++it) {
       if (ALL_ON || tid + 256 * it < CPB) {
-        kreg[it] = buf_ld16(rk, off_k[it] + uint32_t(kb) * bk);
-        vreg[it] = buf_ld16(rv, off_v[it] + uint32_t(kb) * bv);
+        kreg[it] = buf_ld16(rk, off_k0 + uint32_t(kb + RSTEP * it) * bk);
+        vreg[it] = buf_ld16(rv, off_v0 + uint32_t(kb + RSTEP * it) * bv);
       }
     }
   };
@@ -118,8 +167,8 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
 #pragma unroll
     for (int it = 0; it < NK; ++it) {
       if (ALL_ON || tid + 256 * it < CPB) {
-        st16(Kl + off_l[it], kreg[it]);
-        st16(Vl + off_l[it], vreg[it]);
+        st16(Kl + off_l0 + RSTEP * D * it, kreg[it]);
+        st16(Vl + off_l0 + RSTEP * D * it, vreg[it]);
       }
     }
   };
@@ -132,6 +181,11 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     const int kb = qplan_block(plan, i);
     const bool more = i + 1 < plan.nb;
     if (more) gload(qplan_block(plan, i + 1));
+    // the next tile's Q rows into the stash, once this tile's have been read out of it
+    if (kStash && i == 0 && tile + wgs_x < t_hi) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      stash_rows(decode(tile + wgs_x));
+    }
     if (wave_active) {
       const uint16_t* Kl = lds + (i & 1) * BUF;
       const uint16_t* Vl = Kl + BN * D;
@@ -223,8 +277,15 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     if (more) sstore((i + 1) & 1);
     __syncthreads();
   }
+  if (kStash && plan.nb == 0 && tile + wgs_x < t_hi) {  // no key block: stash it here
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    stash_rows(decode(tile + wgs_x));
+  }
+  // the next tile's stash has landed (waited here, before this tile's O stores, which would
+  // otherwise also be waited for)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  if (!wave_active) return;
+  if (!wave_active) continue;
 #pragma unroll
   for (int h = 0; h < HPW; ++h) {
     const float lt = sum_halves(lsum[h]);
@@ -247,15 +308,39 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
           (m2[h] + fast_log2(lt)) * kLn2;
     }
   }
+  }  // tiles
+}
+
+// Resident workgroups per CU of a kernel, remembered per kernel (it depends only on the
+// kernel's resources).
+template <typename K>
+static int fwd_resident_per_cu(K kernel) {
+  static int cached = 0;  // benign race: every thread computes the same value
+  if (cached == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 256, 0) != hipSuccess || n < 1) n = 1;
+    cached = n;
+  }
+  return cached;
+}
+
+template <typename E, int D, int HPW>
+static hipError_t launch_fwd_h(const Args& a, hipStream_t stream) {
+  const int n_tiles = a.n_qtiles * (a.B * a.Hq / (HPW * a.wh));
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < 1)
+    cus = 256;
+  // one resident wave of workgroups, a multiple of the 8 XCDs
+  const int slots = fwd_resident_per_cu(fwd_kernel<E, D, HPW>) * cus;
+  const int wgs = 8 * ((min(n_tiles, slots) + 7) / 8);
+  hipLaunchKernelGGL((fwd_kernel<E, D, HPW>), dim3(wgs), dim3(256), 0, stream, a);
+  return hipGetLastError();
 }
 
 template <typename E, int D>
 static hipError_t launch_fwd_d(const Args& a, int hpw, hipStream_t stream) {
-  const int groups = a.B * a.Hq / (hpw * a.wh);
-  const dim3 grid(a.n_qtiles * groups), block(256);
-  if (hpw == 2) hipLaunchKernelGGL((fwd_kernel<E, D, 2>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((fwd_kernel<E, D, 1>), grid, block, 0, stream, a);
-  return hipGetLastError();
+  return hpw == 2 ? launch_fwd_h<E, D, 2>(a, stream) : launch_fwd_h<E, D, 1>(a, stream);
 }
 
 template <typename E>
