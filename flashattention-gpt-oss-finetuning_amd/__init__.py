@@ -5,16 +5,28 @@ Public surface (drop-in for flash_attention_gpt_oss.py:340-438):
     flash_swda_with_sink(q, k, v, window_size, sink_size=0, is_causal=True, scale=None)
     swa_sink_attention(q, k, v, window_size, sink_size)      # benchmark registry form
 
+GPT-OSS integration (gpt_oss.py): learned per-head sink logits, [B, L, H, D] tensors, full and
+sliding layers, and transformers' attention-function interface:
+    attention(q, k, v, window_size=None, sink_size=0, sinks=None, scale=None, layout="bhld")
+    FlashSWDAWithLearnedSinks.apply(q, k, v, sinks, window_size, sink_size=0, softmax_scale=None)
+    register_transformers("fa_gfx950")   # attn_implementation="fa_gfx950"
+
 The directory name is not a Python identifier; import it with
 ``importlib.import_module("flashattention-gpt-oss-finetuning_amd")`` from the repository root.
 """
-from .attention import FlashSWDAWithSink, flash_swda_with_sink, swa_sink_attention  # noqa: F401
+from .attention import (FlashSWDAWithLearnedSinks, FlashSWDAWithSink, flash_swda_with_sink,  # noqa: F401
+                        swa_sink_attention)
+from .gpt_oss import attention, gpt_oss_attention_forward, register_transformers  # noqa: F401
 from .flops import Workload, allowed_pairs_per_head  # noqa: F401
 
 __all__ = [
     "FlashSWDAWithSink",
     "flash_swda_with_sink",
     "swa_sink_attention",
+    "FlashSWDAWithLearnedSinks",
+    "attention",
+    "gpt_oss_attention_forward",
+    "register_transformers",
     "Workload",
     "allowed_pairs_per_head",
 ]

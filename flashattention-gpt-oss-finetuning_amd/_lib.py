@@ -36,6 +36,8 @@ EXPORTS = (
     "fa_bwd",
     "fa_bwd_dq",
     "fa_bwd_dkdv",
+    "fa_fwd_sinks",
+    "fa_bwd_sinks",
     "fa_bwd_workspace_bytes",
     "fa_check_fwd",
     "fa_check_bwd",
@@ -124,6 +126,11 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(L, name)
                 fn.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
                 fn.restype = ctypes.c_int
+            L.fa_fwd_sinks.argtypes = [ctypes.POINTER(FwdParams), ctypes.c_void_p, ctypes.c_void_p]
+            L.fa_fwd_sinks.restype = ctypes.c_int
+            L.fa_bwd_sinks.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_size_t, ctypes.c_void_p]
+            L.fa_bwd_sinks.restype = ctypes.c_int
             L.fa_bwd_workspace_bytes.argtypes = [ctypes.c_int32] * 7
             L.fa_bwd_workspace_bytes.restype = ctypes.c_size_t
             L.fa_check_fwd.argtypes = [ctypes.POINTER(FwdParams)]

@@ -54,6 +54,22 @@ def _check(tensors, names):
             raise ValueError(f"{n} has dtype {t.dtype} but {names[0]} has {dt}")
 
 
+def _out_like(t: torch.Tensor) -> torch.Tensor:
+    """An output with t's shape, dtype and memory layout (torch.empty_like keeps the strides of a
+    dense tensor, e.g. a [B, L, H, D] buffer viewed as [B, H, L, D]), as the reference allocates
+    o = torch.empty_like(q) (flash_attention_gpt_oss.py:356)."""
+    return torch.empty_like(t)
+
+
+def _sinks_ready(sinks: torch.Tensor, Hq: int, device: torch.device) -> torch.Tensor:
+    """Learned sink logits as the C ABI takes them: float32 [Hq], contiguous, on the device."""
+    if sinks.dim() != 1 or sinks.shape[0] != Hq:
+        raise ValueError(f"sinks must have shape [{Hq}] (one logit per query head), got {tuple(sinks.shape)}")
+    if sinks.device != device:
+        raise RuntimeError(f"sinks is on {sinks.device} but q is on {device}")
+    return sinks.to(torch.float32).contiguous()
+
+
 def _strides3(t: torch.Tensor):
     s = t.stride()
     return (s[0], s[1], s[2])
@@ -84,14 +100,15 @@ class FwdCall:
     """A prepared forward launch: validated inputs, allocated outputs and a filled parameter
     block.  ``run()`` launches on the current stream of the inputs' device."""
 
-    __slots__ = ("params", "inputs", "o", "lse", "device")
+    __slots__ = ("params", "inputs", "o", "lse", "device", "sinks")
 
-    def __init__(self, q, k, v, window: int, sink: int, scale: float):
+    def __init__(self, q, k, v, window: int, sink: int, scale: float, sinks=None):
         _check((q, k, v), ("q", "k", "v"))
         q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
         B, Hq, L, D = q.shape
         Hkv = k.shape[1]
-        self.o = torch.empty((B, Hq, L, D), dtype=q.dtype, device=q.device)
+        self.sinks = None if sinks is None else _sinks_ready(sinks, Hq, q.device)
+        self.o = _out_like(q)
         self.lse = torch.empty((B, Hq, L), dtype=torch.float32, device=q.device)
         self.inputs = (q, k, v)  # keeps the (possibly copied) inputs alive
         self.device = q.device
@@ -112,8 +129,13 @@ class FwdCall:
     def run(self) -> None:
         with _DeviceGuard(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
-            rc = _lib.lib().fa_fwd(ctypes.byref(self.params), ctypes.c_void_p(stream))
-        _lib.raise_for_status(rc, "fa_fwd")
+            if self.sinks is None:
+                rc, fn = _lib.lib().fa_fwd(ctypes.byref(self.params), ctypes.c_void_p(stream)), "fa_fwd"
+            else:
+                rc = _lib.lib().fa_fwd_sinks(ctypes.byref(self.params), ctypes.c_void_p(self.sinks.data_ptr()),
+                                             ctypes.c_void_p(stream))
+                fn = "fa_fwd_sinks"
+        _lib.raise_for_status(rc, fn)
 
 
 def _binding():
@@ -132,13 +154,14 @@ def _binding():
 _BINDING = False
 
 
-def forward(q, k, v, window: int, sink: int, scale: float):
-    """Returns (o, lse) for q [B,Hq,L,D], k/v [B,Hkv,L,D]."""
+def forward(q, k, v, window: int, sink: int, scale: float, sinks=None):
+    """Returns (o, lse) for q [B,Hq,L,D], k/v [B,Hkv,L,D]; `sinks` ([Hq] learned sink logits or
+    None) selects fa_fwd_sinks.  o has q's memory layout."""
     b = _binding()
     if b is not None:
-        o, lse = b.fwd(q, k, v, int(window), int(sink), float(scale))
+        o, lse = b.fwd(q, k, v, int(window), int(sink), float(scale), sinks)
         return o, lse
-    call = FwdCall(q, k, v, window, sink, scale)
+    call = FwdCall(q, k, v, window, sink, scale, sinks)
     call.run()
     return call.o, call.lse
 
@@ -151,17 +174,17 @@ class BwdCall:
     """A prepared backward launch (outputs dq, dk, dv and the workspace allocated once).
     ``run(stage)`` launches fa_bwd ("all"), fa_bwd_dq ("dq") or fa_bwd_dkdv ("dkdv")."""
 
-    __slots__ = ("params", "inputs", "dq", "dk", "dv", "ws", "device")
+    __slots__ = ("params", "inputs", "dq", "dk", "dv", "ws", "device", "sinks", "dsinks")
 
-    def __init__(self, q, k, v, o, lse, do, window: int, sink: int, scale: float):
+    def __init__(self, q, k, v, o, lse, do, window: int, sink: int, scale: float, sinks=None):
         _check((q, k, v, o, do), ("q", "k", "v", "o", "do"))
         q, k, v, o, do = (_kernel_ready(t) for t in (q, k, v, o, do))
         B, Hq, L, D = q.shape
         Hkv = k.shape[1]
         dev = q.device
-        self.dq = torch.empty((B, Hq, L, D), dtype=q.dtype, device=dev)
-        self.dk = torch.empty((B, Hkv, L, D), dtype=k.dtype, device=dev)
-        self.dv = torch.empty((B, Hkv, L, D), dtype=v.dtype, device=dev)
+        self.sinks = None if sinks is None else _sinks_ready(sinks, Hq, dev)
+        self.dsinks = None if sinks is None else torch.empty(Hq, dtype=torch.float32, device=dev)
+        self.dq, self.dk, self.dv = _out_like(q), _out_like(k), _out_like(v)
         ws_bytes = workspace_bytes(B, Hq, Hkv, L, D, window, sink)
         self.ws = torch.empty((max(ws_bytes, 256),), dtype=torch.uint8, device=dev)
         self.inputs = (q, k, v, o, lse, do)
@@ -186,20 +209,28 @@ class BwdCall:
         self.params = p
 
     def run(self, stage: str = "all") -> None:
+        """stage "all" runs fa_bwd, or fa_bwd_sinks when learned sinks were given."""
         fn = {"all": "fa_bwd", "dq": "fa_bwd_dq", "dkdv": "fa_bwd_dkdv"}[stage]
+        ws = (ctypes.c_void_p(self.ws.data_ptr()), ctypes.c_size_t(self.ws.numel()))
         with _DeviceGuard(self.device):
-            stream = torch.cuda.current_stream(self.device).cuda_stream
-            rc = getattr(_lib.lib(), fn)(ctypes.byref(self.params), ctypes.c_void_p(self.ws.data_ptr()),
-                                         ctypes.c_size_t(self.ws.numel()), ctypes.c_void_p(stream))
+            stream = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+            if self.sinks is not None and stage == "all":
+                fn = "fa_bwd_sinks"
+                rc = _lib.lib().fa_bwd_sinks(ctypes.byref(self.params), ctypes.c_void_p(self.sinks.data_ptr()),
+                                             ctypes.c_void_p(self.dsinks.data_ptr()), *ws, stream)
+            else:
+                rc = getattr(_lib.lib(), fn)(ctypes.byref(self.params), *ws, stream)
         _lib.raise_for_status(rc, fn)
 
 
-def backward(q, k, v, o, lse, do, window: int, sink: int, scale: float):
-    """Returns (dq, dk, dv) in the input dtype."""
+def backward(q, k, v, o, lse, do, window: int, sink: int, scale: float, sinks=None):
+    """Returns (dq, dk, dv) in the input dtype, each in the memory layout of q, k, v; with learned
+    `sinks`, (dq, dk, dv, dsinks) with dsinks float32 [Hq]."""
     b = _binding()
     if b is not None:
-        dq, dk, dv = b.bwd(q, k, v, o, lse, do, int(window), int(sink), float(scale))
-        return dq, dk, dv
-    call = BwdCall(q, k, v, o, lse, do, window, sink, scale)
+        return tuple(b.bwd(q, k, v, o, lse, do, int(window), int(sink), float(scale), sinks))
+    call = BwdCall(q, k, v, o, lse, do, window, sink, scale, sinks)
     call.run()
-    return call.dq, call.dk, call.dv
+    if sinks is None:
+        return call.dq, call.dk, call.dv
+    return call.dq, call.dk, call.dv, call.dsinks

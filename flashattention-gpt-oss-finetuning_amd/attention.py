@@ -33,17 +33,7 @@ class FlashSWDAWithSink(torch.autograd.Function):
             raise AssertionError("Currently, only causal attention is supported")
         if softmax_scale is None:
             softmax_scale = 1.0 / math.sqrt(q.shape[-1])
-        batch, n_q_heads, seq_len, head_dim = q.shape
-        _, n_kv_heads, _, _ = k.shape
-        if not (q.shape[0] == v.shape[0] and q.shape[2] == v.shape[2] and q.shape[3] == v.shape[3]):
-            raise AssertionError("Query and Value shapes must be compatible except for num_heads")
-        if not (k.shape[0] == v.shape[0] and k.shape[1] == v.shape[1] and k.shape[2] == v.shape[2]
-                and k.shape[3] == v.shape[3]):
-            raise AssertionError("Key and Value shapes must be the same")
-        if not head_dim <= 128:
-            raise AssertionError("Head dimension must be less than or equal to 128")
-        if not n_q_heads % n_kv_heads == 0:
-            raise AssertionError("Number of query heads must be divisible by number of K/V heads")
+        _check_shapes(q, k, v)
 
         o, lse = _ops.forward(q, k, v, int(window_size), int(sink_size), float(softmax_scale))
 
@@ -59,6 +49,53 @@ class FlashSWDAWithSink(torch.autograd.Function):
         dq, dk, dv = _ops.backward(q, k, v, o, lse, do, int(ctx.window_size), int(ctx.sink_size),
                                    float(ctx.softmax_scale))
         return dq, dk, dv, None, None, None, None
+
+
+class FlashSWDAWithLearnedSinks(torch.autograd.Function):
+    """Causal GQA attention with a sliding window and GPT-OSS learned sink logits.
+
+    forward(q [B,Hq,L,D], k [B,Hkv,L,D], v [B,Hkv,L,D], sinks [Hq], window_size, sink_size=0,
+            softmax_scale=None) -> o [B,Hq,L,D]
+    Every query head h has a learned logit sinks[h] that joins each row's softmax denominator
+    without a value row (GPT-OSS; the reference's sinks are positional only,
+    benchmark_backward_speed.py:45).  window_size None means full causal attention (GPT-OSS's
+    full layers); positional sinks (sink_size) still apply.  The gradient of sinks comes back in
+    sinks' dtype.  Saves (q, k, v, o, lse, sinks); lse includes the sink term.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, sinks, window_size, sink_size=0, softmax_scale=None):
+        if softmax_scale is None:
+            softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+        _check_shapes(q, k, v)
+        if window_size is None:
+            window_size = q.shape[2]
+        o, lse = _ops.forward(q, k, v, int(window_size), int(sink_size), float(softmax_scale), sinks=sinks)
+        ctx.save_for_backward(q, k, v, o, lse, sinks)
+        ctx.softmax_scale = softmax_scale
+        ctx.window_size = window_size
+        ctx.sink_size = sink_size
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse, sinks = ctx.saved_tensors
+        dq, dk, dv, dsinks = _ops.backward(q, k, v, o, lse, do, int(ctx.window_size), int(ctx.sink_size),
+                                           float(ctx.softmax_scale), sinks=sinks)
+        return dq, dk, dv, dsinks.to(sinks.dtype), None, None, None
+
+
+def _check_shapes(q, k, v):
+    """The shape conditions of flash_attention_gpt_oss.py:347-354, same messages."""
+    if not (q.shape[0] == v.shape[0] and q.shape[2] == v.shape[2] and q.shape[3] == v.shape[3]):
+        raise AssertionError("Query and Value shapes must be compatible except for num_heads")
+    if not (k.shape[0] == v.shape[0] and k.shape[1] == v.shape[1] and k.shape[2] == v.shape[2]
+            and k.shape[3] == v.shape[3]):
+        raise AssertionError("Key and Value shapes must be the same")
+    if not q.shape[3] <= 128:
+        raise AssertionError("Head dimension must be less than or equal to 128")
+    if not q.shape[1] % k.shape[1] == 0:
+        raise AssertionError("Number of query heads must be divisible by number of K/V heads")
 
 
 def flash_swda_with_sink(q, k, v, window_size: int, sink_size: int = 0, is_causal: bool = True,

@@ -25,6 +25,11 @@ struct Args {
   // backward workspace
   float* delta;      // [B][Hq][Lp] fp32, Lp = L rounded up to 32
   float* partial;    // sink-key partial sums, see fa_bwd.hip
+  // learned per-head sink logits (GPT-OSS): NULL, or [Hq] fp32 logits that join every row's
+  // softmax denominator without a value row
+  const float* sink_logits;
+  float* dsink;      // backward: [Hq] fp32 gradient of the sink logits (NULL: not computed)
+  float* dsink_part; // backward workspace: [B][Hq][Lp / 32] per-32-row partial sums of dsink
   int64_t sq[3], sk[3], sv[3], so[3], sdo[3], slse[3], sdq[3], sdk[3], sdv[3], so_out[3];
   int B, Hq, Hkv, L, G, Lp;
   int W, S;          // window and sink, clamped to [0, L]
@@ -47,5 +52,6 @@ struct Args {
 hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
 hipError_t launch_bwd_dq(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
 hipError_t launch_bwd_dkdv(const Args& a, int dtype, int D, hipStream_t stream);
+hipError_t launch_bwd_sink_logits(const Args& a, hipStream_t stream);  // after launch_bwd_dq
 
 }  // namespace fa

@@ -19,6 +19,8 @@
 //     instead loops one program over all of L for a sink block,
 //     benchmark_backward_speed.py:432-438).
 //  3. bwd_sink_fold_kernel (only when rows were chunked): adds the sink rows' partial sums.
+//  4. bwd_sink_logit_kernel (only with learned sink logits): adds the dQ kernel's per-row-block
+//     partials of the sink logits' gradient.
 #include <type_traits>
 
 #include "fa_args.h"
@@ -147,6 +149,14 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
     const float ndelta = -delta;
     const float lse2 = q < L ? lse_next * kLog2e : __builtin_inff();
     if (q < L && hf == 0) a.delta[(int64_t(t.b) * a.Hq + t.hw) * a.Lp + q] = delta;
+    if (a.sink_logits && wave_active) {
+      // learned sink: d sink = -sum over rows of P_sink * delta, P_sink = 2^(sink*log2e - lse2);
+      // one partial per 32-row block, summed in a fixed order by bwd_sink_logit_kernel
+      float v = q < L ? fast_exp2(a.sink_logits[t.hw] * kLog2e - lse2) * delta : 0.f;
+#pragma unroll
+      for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+      if (lane == 0) a.dsink_part[(int64_t(t.b) * a.Hq + t.hw) * (a.Lp / 32) + qw / 32] = -v;
+    }
 
     f32x16 acc[DB];
 #pragma unroll
@@ -687,6 +697,28 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
       uint16_t(pk >> 16);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Gradient of the learned sink logits: dsink[h] = sum over (b, 32-row block) of the dQ kernel's
+// partials, in a fixed order (each thread strides over the partials in order, then the waves'
+// sums are combined in wave order), so reruns are bitwise identical.  One workgroup per head.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bwd_sink_logit_kernel(const Args a) {
+  __shared__ float wsum[4];
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int nb = a.Lp / 32;
+  const int64_t n = int64_t(a.B) * nb;
+  float acc = 0.f;
+  for (int64_t i = tid; i < n; i += 256) {
+    const int64_t b = i / nb, j = i % nb;
+    acc += a.dsink_part[(b * a.Hq + h) * nb + j];
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  if ((tid & 63) == 0) wsum[tid >> 6] = acc;
+  __syncthreads();
+  if (tid == 0) a.dsink[h] = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+}
+
 // Resident workgroups per CU of a kernel (hipOccupancyMaxActiveBlocksPerMultiprocessor,
 // 256 threads), remembered per kernel: it depends only on the kernel's resources.
 template <typename K>
@@ -748,6 +780,10 @@ hipError_t launch_bwd_dq(const Args& a, int dtype, int D, int hpw, hipStream_t s
 }
 hipError_t launch_bwd_dkdv(const Args& a, int dtype, int D, hipStream_t s) {
   return dtype == 1 ? dkdv_e<BF16>(a, D, s) : dkdv_e<F16>(a, D, s);
+}
+hipError_t launch_bwd_sink_logits(const Args& a, hipStream_t s) {
+  hipLaunchKernelGGL(bwd_sink_logit_kernel, dim3(a.Hq), dim3(256), 0, s, a);
+  return hipGetLastError();
 }
 
 }  // namespace fa

@@ -86,6 +86,9 @@ SinkPlan sink_plan(int L, int W, int S) {
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// per-32-row-block partial sums of the learned sink logits' gradient: [B][Hq][Lp / 32] fp32
+size_t dsink_part_bytes(int B, int Hq, int L) { return align256(size_t(B) * Hq * ((size_t(L) + 31) / 32) * sizeof(float)); }
+
 size_t delta_bytes(int B, int Hq, int L) {
   const size_t Lp = (size_t(L) + 31) / 32 * 32;
   return align256(size_t(B) * Hq * Lp * sizeof(float));
@@ -165,9 +168,11 @@ int fa_check_bwd(const fa_bwd_params* p) {
   return FA_OK;
 }
 
-int fa_fwd(const fa_fwd_params* p, void* stream) {
-  const int rc = fa_check_fwd(p);
-  if (rc != FA_OK) return rc;
+}  // extern "C"
+
+namespace {
+
+int run_fwd(const fa_fwd_params* p, const float* sinks, void* stream) {
   fa::Args a = base_args(p->batch, p->heads_q, p->heads_kv, p->seqlen, p->head_dim, p->window, p->sink,
                          p->softmax_scale);
   a.q = p->q;
@@ -175,6 +180,7 @@ int fa_fwd(const fa_fwd_params* p, void* stream) {
   a.v = p->v;
   a.o_out = p->o;
   a.lse_out = p->lse;
+  a.sink_logits = sinks;
   copy3(a.sq, p->q_stride);
   copy3(a.sk, p->k_stride);
   copy3(a.sv, p->v_stride);
@@ -189,12 +195,30 @@ int fa_fwd(const fa_fwd_params* p, void* stream) {
   return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 
+}  // namespace
+
+extern "C" {
+
+int fa_fwd(const fa_fwd_params* p, void* stream) {
+  const int rc = fa_check_fwd(p);
+  return rc != FA_OK ? rc : run_fwd(p, nullptr, stream);
+}
+
+int fa_fwd_sinks(const fa_fwd_params* p, const float* sinks, void* stream) {
+  const int rc = fa_check_fwd(p);
+  if (rc != FA_OK) return rc;
+  if (!sinks) return FA_ERR_NULL;
+  if (!aligned4(sinks)) return FA_ERR_ALIGN;
+  return run_fwd(p, sinks, stream);
+}
+
 size_t fa_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seqlen,
                               int32_t head_dim, int32_t window, int32_t sink) {
   if (check_common(batch, heads_q, heads_kv, seqlen, head_dim, window, sink, 1.f, FA_DTYPE_BF16) != FA_OK)
     return 0;
   const SinkPlan sp = sink_plan(seqlen, window, sink);
-  return delta_bytes(batch, heads_q, seqlen) + partial_bytes(batch, heads_kv, head_dim, sp);
+  return delta_bytes(batch, heads_q, seqlen) + partial_bytes(batch, heads_kv, head_dim, sp) +
+         dsink_part_bytes(batch, heads_q, seqlen);
 }
 
 }  // extern "C"
@@ -240,6 +264,8 @@ int prepare_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
   const SinkPlan sp = sink_plan(a.L, p->window, p->sink);
   char* ws = static_cast<char*>(workspace);
   a.partial = reinterpret_cast<float*>(ws + delta_bytes(a.B, a.Hq, a.L));
+  a.dsink_part = reinterpret_cast<float*>(ws + delta_bytes(a.B, a.Hq, a.L) +
+                                          partial_bytes(a.B, a.Hkv, p->head_dim, sp));
   a.n_kblocks = (a.L + fa::kKvKeys - 1) / fa::kKvKeys;
   a.nsp = sp.nsp;
   a.n_chunks = sp.n_chunks;
@@ -270,6 +296,22 @@ int fa_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int r1 = run_dq(a, p, hpw, s);
   return r1 != FA_OK ? r1 : run_dkdv(a, p, s);
+}
+
+int fa_bwd_sinks(const fa_bwd_params* p, const float* sinks, float* dsinks, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  fa::Args a;
+  int hpw = 1;
+  const int rc = prepare_bwd(p, workspace, workspace_bytes, &a, &hpw);
+  if (rc != FA_OK) return rc;
+  if (!sinks || !dsinks) return FA_ERR_NULL;
+  if (!aligned4(sinks) || !aligned4(dsinks)) return FA_ERR_ALIGN;
+  a.sink_logits = sinks;
+  a.dsink = dsinks;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int r = run_dq(a, p, hpw, s);
+  if (r == FA_OK) r = fa::launch_bwd_sink_logits(a, s) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+  return r != FA_OK ? r : run_dkdv(a, p, s);
 }
 
 int fa_bwd_dq(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {

@@ -288,9 +288,19 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   if (!wave_active) continue;
 #pragma unroll
   for (int h = 0; h < HPW; ++h) {
-    const float lt = sum_halves(lsum[h]);
+    float lt = sum_halves(lsum[h]);
     if (q >= L) continue;
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    float mt = m2[h], r = 1.f;
+    if (a.sink_logits) {
+      // the learned sink joins the denominator: l' = l 2^(m - m') + 2^(sink*log2e - m'), with
+      // m' = max(m, sink*log2e) so that neither term overflows
+      const float sl = a.sink_logits[hw + h] * kLog2e;
+      const float mn = fmaxf(mt, sl);
+      r = fast_exp2(mt - mn);
+      lt = lt * r + fast_exp2(sl - mn);
+      mt = mn;
+    }
+    const float inv = lt > 0.f ? r / lt : 0.f;
     char* op = reinterpret_cast<char*>(a.o_out) +
                2 * (int64_t(b) * a.so_out[0] + int64_t(hw + h) * a.so_out[1] + int64_t(q) * a.so_out[2]);
 #pragma unroll
@@ -305,7 +315,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     }
     if (hf == 0) {
       a.lse_out[int64_t(b) * a.slse[0] + int64_t(hw + h) * a.slse[1] + int64_t(q) * a.slse[2]] =
-          (m2[h] + fast_log2(lt)) * kLn2;
+          (mt + fast_log2(lt)) * kLn2;
     }
   }
   }  // tiles

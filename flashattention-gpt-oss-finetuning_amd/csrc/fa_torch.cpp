@@ -4,7 +4,8 @@
 // caching allocator), the current HIP stream, filling fa_fwd_params / fa_bwd_params and the
 // launch -- in C++, so a forward + backward costs a few microseconds of host time instead of
 // the tens that per-field ctypes marshalling takes.  Every FLOP still runs in libfa_gfx950.so;
-// this module only calls fa_fwd / fa_bwd / fa_bwd_workspace_bytes / fa_strerror.
+// this module only calls fa_fwd / fa_bwd / fa_fwd_sinks / fa_bwd_sinks / fa_bwd_workspace_bytes /
+// fa_strerror.
 //
 // Error behaviour matches the ctypes path (_ops.py): tensors not on a GPU -> RuntimeError,
 // unsupported dtype or shape -> ValueError, a C ABI status -> ValueError (argument) or
@@ -78,14 +79,27 @@ void* current_stream(const at::Tensor& t) {
   return c10::hip::getCurrentHIPStream(t.device().index()).stream();
 }
 
-// forward: returns (o, lse) for q [B,Hq,L,D], k/v [B,Hkv,L,D]
+// Learned sink logits as the C ABI takes them: float32 [Hq], contiguous, on q's device.
+at::Tensor sinks_ready(const at::Tensor& sinks, int64_t Hq, const at::Tensor& q) {
+  if (sinks.dim() != 1 || sinks.size(0) != Hq)
+    throw std::invalid_argument("sinks must have shape [" + std::to_string(Hq) +
+                                "] (one logit per query head)");
+  if (sinks.device() != q.device())
+    throw std::runtime_error("sinks is on " + sinks.device().str() + " but q is on " + q.device().str());
+  return sinks.to(at::kFloat).contiguous();
+}
+
+// forward: returns (o, lse) for q [B,Hq,L,D], k/v [B,Hkv,L,D]; o has q's memory layout (as
+// torch.empty_like(q) in the reference, flash_attention_gpt_oss.py:356).  With learned sink
+// logits (float32-convertible [Hq]) it calls fa_fwd_sinks.
 std::vector<at::Tensor> fwd(const at::Tensor& q_in, const at::Tensor& k_in, const at::Tensor& v_in, int64_t window,
-                            int64_t sink, double scale) {
+                            int64_t sink, double scale, const c10::optional<at::Tensor>& sinks_in) {
   check({{&q_in, "q"}, {&k_in, "k"}, {&v_in, "v"}});
   const c10::DeviceGuard guard(q_in.device());
   const at::Tensor q = kernel_ready(q_in), k = kernel_ready(k_in), v = kernel_ready(v_in);
   const int64_t B = q.size(0), Hq = q.size(1), L = q.size(2), D = q.size(3);
-  at::Tensor o = at::empty({B, Hq, L, D}, q.options());
+  const at::Tensor sinks = sinks_in.has_value() ? sinks_ready(*sinks_in, Hq, q) : at::Tensor();
+  at::Tensor o = at::empty_like(q);
   at::Tensor lse = at::empty({B, Hq, L}, q.options().dtype(at::kFloat));
   fa_fwd_params p{};
   p.q = q.data_ptr();
@@ -109,22 +123,27 @@ std::vector<at::Tensor> fwd(const at::Tensor& q_in, const at::Tensor& k_in, cons
   p.sink = clamp_i32(sink);
   p.softmax_scale = float(scale);
   p.dtype = dtype_code(q);
-  raise_for_status(fa_fwd(&p, current_stream(q)), "fa_fwd");
+  if (sinks.defined())
+    raise_for_status(fa_fwd_sinks(&p, sinks.data_ptr<float>(), current_stream(q)), "fa_fwd_sinks");
+  else
+    raise_for_status(fa_fwd(&p, current_stream(q)), "fa_fwd");
   return {o, lse};
 }
 
-// backward: returns (dq, dk, dv) in the input dtype
+// backward: returns (dq, dk, dv) in the input dtype and the layouts of q, k, v; with learned
+// sink logits, (dq, dk, dv, dsinks) through fa_bwd_sinks, dsinks float32 [Hq]
 std::vector<at::Tensor> bwd(const at::Tensor& q_in, const at::Tensor& k_in, const at::Tensor& v_in,
                             const at::Tensor& o_in, const at::Tensor& lse, const at::Tensor& do_in, int64_t window,
-                            int64_t sink, double scale) {
+                            int64_t sink, double scale, const c10::optional<at::Tensor>& sinks_in) {
   check({{&q_in, "q"}, {&k_in, "k"}, {&v_in, "v"}, {&o_in, "o"}, {&do_in, "do"}});
   const c10::DeviceGuard guard(q_in.device());
   const at::Tensor q = kernel_ready(q_in), k = kernel_ready(k_in), v = kernel_ready(v_in);
   const at::Tensor o = kernel_ready(o_in), dout = kernel_ready(do_in);
   const int64_t B = q.size(0), Hq = q.size(1), L = q.size(2), D = q.size(3), Hkv = k.size(1);
-  at::Tensor dq = at::empty({B, Hq, L, D}, q.options());
-  at::Tensor dk = at::empty({B, Hkv, L, D}, k.options());
-  at::Tensor dv = at::empty({B, Hkv, L, D}, v.options());
+  const at::Tensor sinks = sinks_in.has_value() ? sinks_ready(*sinks_in, Hq, q) : at::Tensor();
+  at::Tensor dq = at::empty_like(q);
+  at::Tensor dk = at::empty_like(k);
+  at::Tensor dv = at::empty_like(v);
   const size_t ws_bytes = fa_bwd_workspace_bytes(clamp_i32(B), clamp_i32(Hq), clamp_i32(Hkv), clamp_i32(L),
                                                  clamp_i32(D), clamp_i32(window), clamp_i32(sink));
   at::Tensor ws = at::empty({int64_t(ws_bytes > 256 ? ws_bytes : 256)}, q.options().dtype(at::kByte));
@@ -158,6 +177,13 @@ std::vector<at::Tensor> bwd(const at::Tensor& q_in, const at::Tensor& k_in, cons
   p.sink = clamp_i32(sink);
   p.softmax_scale = float(scale);
   p.dtype = dtype_code(q);
+  if (sinks.defined()) {
+    at::Tensor dsinks = at::empty({Hq}, q.options().dtype(at::kFloat));
+    raise_for_status(fa_bwd_sinks(&p, sinks.data_ptr<float>(), dsinks.data_ptr<float>(), ws.data_ptr(),
+                                  size_t(ws.numel()), current_stream(q)),
+                     "fa_bwd_sinks");
+    return {dq, dk, dv, dsinks};
+  }
   raise_for_status(fa_bwd(&p, ws.data_ptr(), size_t(ws.numel()), current_stream(q)), "fa_bwd");
   return {dq, dk, dv};
 }
@@ -166,6 +192,9 @@ std::vector<at::Tensor> bwd(const at::Tensor& q_in, const at::Tensor& k_in, cons
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "PyTorch binding of libfa_gfx950.so (fa_fwd / fa_bwd)";
-  m.def("fwd", &fwd, "forward: (q, k, v, window, sink, scale) -> (o, lse)");
-  m.def("bwd", &bwd, "backward: (q, k, v, o, lse, do, window, sink, scale) -> (dq, dk, dv)");
+  m.def("fwd", &fwd, "forward: (q, k, v, window, sink, scale, sinks=None) -> (o, lse)", py::arg("q"), py::arg("k"),
+        py::arg("v"), py::arg("window"), py::arg("sink"), py::arg("scale"), py::arg("sinks") = py::none());
+  m.def("bwd", &bwd, "backward: (q, k, v, o, lse, do, window, sink, scale, sinks=None) -> (dq, dk, dv[, dsinks])",
+        py::arg("q"), py::arg("k"), py::arg("v"), py::arg("o"), py::arg("lse"), py::arg("do"), py::arg("window"),
+        py::arg("sink"), py::arg("scale"), py::arg("sinks") = py::none());
 }

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define FA_GFX950_VERSION 10000 /* 1.0.0 */
+#define FA_GFX950_VERSION 10100 /* 1.1.0 */
 
 /* Element types of q/k/v/o/dout/dq/dk/dv.  All of them share one type per call. */
 enum fa_dtype { FA_DTYPE_BF16 = 1, FA_DTYPE_F16 = 2 };
@@ -112,8 +112,9 @@ typedef struct fa_bwd_params {
 /* Launches the forward kernel.  Returns FA_OK or a negative fa_status. */
 int fa_fwd(const fa_fwd_params* p, void* stream);
 
-/* Bytes of device workspace fa_bwd needs for this problem (row statistics of the backward and
- * per-chunk partial sums for the sink keys).  Returns 0 for an invalid problem.  The
+/* Bytes of device workspace fa_bwd / fa_bwd_sinks need for this problem (row statistics of the
+ * backward, per-chunk partial sums for the sink keys and per-row-block partial sums of the
+ * learned sinks' gradient).  Returns 0 for an invalid problem.  The
  * reference instead allocates fp32 dK/dV staging buffers inside backward
  * (flash_attention_gpt_oss.py:397-400). */
 size_t fa_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t seqlen,
@@ -132,6 +133,25 @@ int fa_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void
  * must run after fa_bwd_dq on the same workspace, in stream order. */
 int fa_bwd_dq(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
 int fa_bwd_dkdv(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Learned attention sinks (GPT-OSS).  The reference has no such entry point: its sinks are the
+ * first S key positions (benchmark_backward_speed.py:45, README.md:15).  GPT-OSS models instead
+ * give every query head h a learned logit sinks[h] that joins each row's softmax denominator
+ * without a value row:
+ *     P[q, k] = exp(s[q, k] - lse[q]),
+ *     lse[q]  = log( sum over allowed k of exp(s[q, k])  +  exp(sinks[h]) ),
+ * which is the eager GptOssAttention path of HF transformers (the logits get one more column
+ * holding the sink, are softmaxed, and the column is dropped).  The window and the positional
+ * sinks of p still apply; GPT-OSS itself uses p->sink = 0 with window 128 (sliding layers) or
+ * window >= L (full layers).  sinks is float32 [Hq], 4-byte aligned.
+ * fa_fwd_sinks writes o and an lse that includes the sink term; fa_bwd_sinks must get that lse.
+ * fa_bwd_sinks computes dq, dk and dv as fa_bwd does, and writes
+ *     dsinks[h] = - sum over b, q of P_sink[b, h, q] * delta[b, h, q],
+ *     P_sink = exp(sinks[h] - lse),  delta = rowsum(dout * o),
+ * to dsinks (float32 [Hq], overwritten; summed in a fixed order, so reruns are identical). */
+int fa_fwd_sinks(const fa_fwd_params* p, const float* sinks, void* stream);
+int fa_bwd_sinks(const fa_bwd_params* p, const float* sinks, float* dsinks, void* workspace,
+                 size_t workspace_bytes, void* stream);
 
 /* Host-only argument checks used by fa_fwd / fa_bwd (no HIP call is made). */
 int fa_check_fwd(const fa_fwd_params* p);

@@ -56,6 +56,23 @@ def attention_fwd_bwd(q, k, v, do, window_size: int, sink_size: int, scale: Opti
     memory stays at row_chunk x L scores.  `heads` optionally restricts the query heads that
     are evaluated (dq/o/lse of other heads stay 0; dk/dv then only sum the listed heads).
     """
+    return _fwd_bwd(q, k, v, do, window_size, sink_size, scale, compute_dtype, row_chunk, heads, None)[:5]
+
+
+@torch.no_grad()
+def attention_fwd_bwd_sinks(q, k, v, sinks, do, window_size: int, sink_size: int = 0,
+                            scale: Optional[float] = None, compute_dtype=torch.float32,
+                            row_chunk: Optional[int] = None, heads=None):
+    """attention_fwd_bwd with GPT-OSS learned sinks: `sinks` [Hq] holds one logit per query head
+    that joins every row's softmax denominator without a value row (the eager GptOssAttention
+    path of HF transformers, restated by gpt_oss_eager below):
+      lse = log(sum_k exp(s) + exp(sink)),  P = exp(s - lse),  P_sink = exp(sink - lse),
+      dsink = -sum over batch and rows of P_sink * delta.
+    Returns (o, lse, dq, dk, dv, dsinks)."""
+    return _fwd_bwd(q, k, v, do, window_size, sink_size, scale, compute_dtype, row_chunk, heads, sinks)
+
+
+def _fwd_bwd(q, k, v, do, window_size, sink_size, scale, compute_dtype, row_chunk, heads, sinks):
     B, Hq, L, D = q.shape
     Hkv = k.shape[1]
     group = Hq // Hkv
@@ -68,6 +85,8 @@ def attention_fwd_bwd(q, k, v, do, window_size: int, sink_size: int, scale: Opti
     dq = torch.zeros_like(qf)
     dk = torch.zeros_like(kf)
     dv = torch.zeros_like(vf)
+    sk = None if sinks is None else sinks.to(compute_dtype)
+    dsinks = None if sinks is None else torch.zeros(Hq, dtype=compute_dtype, device=q.device)
     pos = torch.arange(L, device=q.device)
     head_list = range(Hq) if heads is None else heads
     for b in range(B):
@@ -84,17 +103,40 @@ def attention_fwd_bwd(q, k, v, do, window_size: int, sink_size: int, scale: Opti
                 s = torch.matmul(Q, Kt) * scale
                 s = s.masked_fill(~keep, float("-inf"))
                 m = torch.logsumexp(s, dim=-1)
+                if sk is not None:
+                    m = torch.logaddexp(m, sk[h].expand_as(m))
                 p = torch.exp(s - m.view(-1, 1))
                 ob = torch.matmul(p, V)
                 dp = torch.matmul(G, Vt)
                 delta = (G * ob).sum(dim=-1, keepdim=True)
                 ds = p * (dp - delta)
+                if sk is not None:
+                    dsinks[h] -= (torch.exp(sk[h] - m) * delta.view(-1)).sum()
                 o[b, h, r0:r1] = ob
                 lse[b, h, r0:r1] = m
                 dq[b, h, r0:r1] = torch.matmul(ds, K) * scale
                 dk[b, g] += torch.matmul(ds.t().contiguous(), Q) * scale
                 dv[b, g] += torch.matmul(p.t().contiguous(), G)
-    return o, lse, dq, dk, dv
+    return o, lse, dq, dk, dv, dsinks
+
+
+def gpt_oss_eager(q, k, v, sinks, window_size: Optional[int], scale: float):
+    """The eager GPT-OSS attention of HF transformers (modeling_gpt_oss.py eager_attention_forward),
+    restated on [B, H, L, D] tensors in their own dtype: repeated K/V, scaled scores plus the
+    causal (and sliding, q - k < window) mask, the sink logit appended as one more column,
+    softmax, the column dropped, P @ V.  Returns o [B, Hq, L, D]; autograd gives its backward."""
+    group = q.shape[1] // k.shape[1]
+    k = expand_kv(k, group)
+    v = expand_kv(v, group)
+    L = q.shape[2]
+    scores = torch.matmul(q, k.transpose(-1, -2).contiguous()) * scale
+    keep = allowed_mask(L, L if window_size is None else window_size, 0, device=q.device)
+    scores = scores.masked_fill(~keep, float("-inf"))
+    col = sinks.to(scores.dtype).reshape(1, -1, 1, 1).expand(q.shape[0], -1, L, 1)
+    logits = torch.cat([scores, col], dim=-1)
+    logits = logits - logits.max(dim=-1, keepdim=True).values
+    probs = torch.softmax(logits, dim=-1)[..., :-1]
+    return torch.matmul(probs.to(v.dtype), v)
 
 
 class OracleAttention(torch.autograd.Function):
@@ -115,3 +157,23 @@ class OracleAttention(torch.autograd.Function):
         window_size, sink_size, scale = ctx.cfg
         _, _, dq, dk, dv = attention_fwd_bwd(q, k, v, do, window_size, sink_size, scale, compute_dtype=q.dtype)
         return dq, dk, dv, None, None, None
+
+
+class OracleAttentionSinks(torch.autograd.Function):
+    """attention_fwd_bwd_sinks behind autograd (float64 on CPU), for gradcheck of the sink
+    logits' gradient as well as dq, dk, dv."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, sinks, window_size, sink_size, scale):
+        ctx.save_for_backward(q, k, v, sinks)
+        ctx.cfg = (window_size, sink_size, scale)
+        return attention_fwd_bwd_sinks(q, k, v, sinks, torch.zeros_like(q), window_size, sink_size, scale,
+                                       compute_dtype=q.dtype)[0]
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, sinks = ctx.saved_tensors
+        window_size, sink_size, scale = ctx.cfg
+        _, _, dq, dk, dv, ds = attention_fwd_bwd_sinks(q, k, v, sinks, do, window_size, sink_size, scale,
+                                                        compute_dtype=q.dtype)
+        return dq, dk, dv, ds, None, None, None

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_strerror():
     L = _lib.lib()
-    assert L.fa_version() == 10000
+    assert L.fa_version() == 10100
     codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10]
     texts = [_lib.strerror(c) for c in codes]
     assert len(set(texts)) == len(codes)
@@ -191,22 +191,34 @@ def test_entry_points_reject_before_any_hip_call():
     need = L.fa_bwd_workspace_bytes(1, 8, 2, 128, 64, 16, 4)
     assert L.fa_bwd(ctypes.byref(_bwd_params()), ctypes.c_void_p(1 << 20), need - 1, None) == _lib.FA_ERR_WORKSPACE
     assert L.fa_bwd(ctypes.byref(_bwd_params()), ctypes.c_void_p((1 << 20) + 16), need, None) == _lib.FA_ERR_WORKSPACE
+    # learned-sink entry points: the parameter checks first, then the sink pointers
+    assert L.fa_fwd_sinks(ctypes.byref(_fwd_params(head_dim=48)), ctypes.c_void_p(256), None) == _lib.FA_ERR_HEAD_DIM
+    assert L.fa_fwd_sinks(ctypes.byref(_fwd_params()), None, None) == _lib.FA_ERR_NULL
+    assert L.fa_fwd_sinks(ctypes.byref(_fwd_params()), ctypes.c_void_p(258), None) == _lib.FA_ERR_ALIGN
+    ws_ok = (ctypes.c_void_p(1 << 20), need)
+    assert L.fa_bwd_sinks(ctypes.byref(_bwd_params()), ctypes.c_void_p(256), ctypes.c_void_p(512), None, 0,
+                          None) == _lib.FA_ERR_WORKSPACE
+    assert L.fa_bwd_sinks(ctypes.byref(_bwd_params()), None, ctypes.c_void_p(512), *ws_ok, None) == _lib.FA_ERR_NULL
+    assert L.fa_bwd_sinks(ctypes.byref(_bwd_params()), ctypes.c_void_p(256), None, *ws_ok, None) == _lib.FA_ERR_NULL
+    assert L.fa_bwd_sinks(ctypes.byref(_bwd_params()), ctypes.c_void_p(256), ctypes.c_void_p(514), *ws_ok,
+                          None) == _lib.FA_ERR_ALIGN
 
 
 def test_workspace_bytes():
     L = _lib.lib()
     ws = L.fa_bwd_workspace_bytes
     # delta: B*Hq*round_up(L, 32) floats, 256-aligned; no sink split when every row is within
-    # the window of the sink block
-    assert ws(1, 8, 2, 128, 64, 200, 4) == 8 * 128 * 4
-    assert ws(1, 8, 2, 100, 64, 200, 4) == 8 * 128 * 4
+    # the window of the sink block; the learned-sink partials: B*Hq*ceil(L/32) floats, 256-aligned
+    assert ws(1, 8, 2, 128, 64, 200, 4) == 8 * 128 * 4 + 256
+    assert ws(1, 8, 2, 100, 64, 200, 4) == 8 * 128 * 4 + 256
     # sink split: 1 block of 64 keys; its window ends at row 191, chunks of 64 rows start at 160
     # (rounded down to 32): ceil((4096 - 160) / 64) = 62 chunks + the regular slot, dK and dV,
     # S = 4 sink rows x D fp32 each
     L_, D = 4096, 64
     expect_delta = 64 * 4096 * 4
     expect_partial = 8 * 1 * (62 + 1) * 2 * 4 * D * 4
-    assert ws(1, 64, 8, L_, D, 128, 4) == expect_delta + expect_partial
+    expect_dsink = 64 * (4096 // 32) * 4
+    assert ws(1, 64, 8, L_, D, 128, 4) == expect_delta + expect_partial + expect_dsink
     # invalid problems give 0
     assert ws(1, 8, 3, 128, 64, 16, 4) == 0
     assert ws(1, 8, 2, 128, 64, 0, 0) == 0
