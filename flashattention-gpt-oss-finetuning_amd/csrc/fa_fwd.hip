@@ -43,7 +43,10 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF + 4 * STASH];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  // wave-uniform in a scalar register, so that per-wave rows, heads and buffer descriptors stay
+  // scalar (no per-lane copies, no waterfall loops around buffer loads)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hf = lane >> 5;
   const int L = a.L, W = a.W, S = a.S;
 
