@@ -46,6 +46,11 @@ struct Args {
   int chunk_rows;
   int n_chunk_wgs;   // B * Hkv * nsp * n_chunks
   int srows;         // sink rows stored per block in the partial sums: min(S, 64)
+  // sink rows in the dQ kernel (dq_sink_mode): rows >= sink_row0 add the sink keys' dK/dV there
+  int sink_dq;       // 1 in that mode
+  int sink_row0;
+  float* dq_sink_part;  // [n_tiles][dK, dV][srows][D] fp32: a run's sums at the slot of its first tile
+  int dq_wgs;           // the dQ kernel's grid (set for the sink fold)
 };
 
 // Launchers (return the hipError_t of the launch; launch_bwd_dkdv also launches the sink fold).

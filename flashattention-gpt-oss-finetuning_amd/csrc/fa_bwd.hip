@@ -38,9 +38,18 @@ namespace fa {
 // tiles (neighbouring tiles share K/V rows in that XCD's L2) and its workgroups walk it with the
 // XCD's workgroup count as stride.  The rows of a workgroup's next tile (Q, dO, O, lse) are
 // loaded while the current tile computes, so the row traffic overlaps the MFMA work.
+//
+// SINK (dq_sink_mode, S <= 16 sink keys): rows past key block 0's window see the sink keys only
+// through the sink block, which this kernel visits for every tile anyway.  Their contributions to
+// the sink keys' gradients, dV_s += P^T dO and dK_s += dS^T Q over keys [0, 16), accumulate here
+// (v_mfma_f32_16x16x32, the tile's 32 rows as the reduction): P and dS of keys [0, 16) go through
+// a per-wave LDS tile [32 rows][16 keys] to become the A operand, and dO / Q are read transposed
+// from the wave's row-major stash tiles.  The accumulators are summed over the workgroup's waves
+// and written once per run of tiles of one KV group (see the flush below), so the key-major
+// kernel needs no workgroups for those rows.
 // ---------------------------------------------------------------------------------------------
-template <typename E, int D>
-__global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
+template <typename E, int D, bool SINK>
+__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   constexpr int BN = 64;
   constexpr int KS = D / 16;
   constexpr int DB = D >= 32 ? D / 32 : 1;
@@ -49,8 +58,13 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
   constexpr int NK = (CPB + 255) / 256;    // chunks per thread
   constexpr bool ALL_ON = CPB >= 256;      // every thread loads a chunk of every tile
   constexpr int NX = 8;                    // XCDs: workgroup i runs on XCD i % 8
-  constexpr int STASH = 3 * KS * 512;      // per wave: the next tile's Q, dO, O fragments
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF + 4 * STASH];
+  constexpr int TILE = 32 * D;             // one 32-row tile, swizzled row-major [row][d]
+  constexpr int STASH = 3 * TILE;          // per wave: the next tile's Q, dO, O tiles
+  constexpr int NB16 = D / 16;             // 16-column blocks of the sink accumulators
+  // the P / dS transposition tiles of the sink path: in the wave's O tile (read only for delta at
+  // the start of a tile), or, for D = 16 where that tile is too small, in a region of their own
+  constexpr int PT_EXTRA = (SINK && D < 32) ? 4 * 1024 : 0;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF + 4 * STASH + PT_EXTRA];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -66,6 +80,8 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
   const int xcd = blockIdx.x % NX, pos = blockIdx.x / NX, wgs_x = gridDim.x / NX;
   const int per = n_tiles / NX, rem = n_tiles % NX;
   const int t_lo = xcd * per + min(xcd, rem), t_hi = t_lo + per + (xcd < rem ? 1 : 0);
+  // tiles per (batch, KV head): n_qtiles row tiles of each of the G / wh head groups
+  const int tiles_per_kv = a.n_qtiles * (a.G / a.wh);
 
   // tile -> (b, KV head, this wave's head hw, first row qw)
   struct TileIdx {
@@ -84,25 +100,27 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
     return t;
   };
 
-  // The rows of a tile for this wave: Q, dO and O fragments (lane = row, head-dim slice
-  // [hf*D/2 + 8ks, +8)) go by LDS DMA into the wave's own stash -- fragment (tensor x, ks) of
-  // lane l at 16 bytes each, in lane order -- so they occupy no registers while the current
-  // tile computes; the row's lse goes to a register.  Buffer resources over the head's rows
-  // [0, L): rows past L read as zero.
+  // The rows of a tile for this wave: Q, dO and O go by LDS DMA into the wave's own stash as
+  // swizzled row-major [32][D] tiles (DMA instruction p, lane l fills 16-byte position 64p + l, so
+  // it loads the global chunk that the swizzle places there), where they occupy no registers
+  // while the current tile computes; the row's lse goes to a register.  Buffer resources over the
+  // head's rows [0, L): rows past L read as zero.
   uint16_t* stash = lds + 2 * BUF + wave * STASH;
   const uint32_t nq = span_bytes(L, a.sq[2], D), nd = span_bytes(L, a.sdo[2], D), no = span_bytes(L, a.so[2], D);
   const uint32_t nl = uint32_t((int64_t(L - 1) * a.slse[2] + 1) * 4);
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
   auto stash_rows = [&](const TileIdx& t) {
     const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(a.q) + 2 * (int64_t(t.b) * a.sq[0] + int64_t(t.hw) * a.sq[1]), nq);
     const rsrc_t rd = make_rsrc(reinterpret_cast<const char*>(a.dout) + 2 * (int64_t(t.b) * a.sdo[0] + int64_t(t.hw) * a.sdo[1]), nd);
     const rsrc_t ro = make_rsrc(reinterpret_cast<const char*>(a.o) + 2 * (int64_t(t.b) * a.so[0] + int64_t(t.hw) * a.so[1]), no);
-    const int q = t.qw + r32;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int d = hf * (D / 2) + 8 * ks;
-      buf_dma16(rq, stash + (0 * KS + ks) * 512, uint32_t((int64_t(q) * a.sq[2] + d) * 2));
-      buf_dma16(rd, stash + (1 * KS + ks) * 512, uint32_t((int64_t(q) * a.sdo[2] + d) * 2));
-      buf_dma16(ro, stash + (2 * KS + ks) * 512, uint32_t((int64_t(q) * a.so[2] + d) * 2));
+    for (int p = 0; p < KS; ++p) {
+      const int tr = (64 * p + lane) / CPR;  // tile row of this lane's 16-byte position
+      const int col = 8 * (((64 * p + lane) % CPR) ^ swz<D>(tr));
+      const int64_t row = t.qw + tr;
+      buf_dma16(rq, stash + 0 * TILE + 512 * p, uint32_t((row * a.sq[2] + col) * 2));
+      buf_dma16(rd, stash + 1 * TILE + 512 * p, uint32_t((row * a.sdo[2] + col) * 2));
+      buf_dma16(ro, stash + 2 * TILE + 512 * p, uint32_t((row * a.so[2] + col) * 2));
     }
   };
   auto load_lse = [&](const TileIdx& t) {
@@ -124,7 +142,19 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
   const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
   const uint32_t nk_bytes = span_bytes(L, a.sk[2], D), nv_bytes = span_bytes(L, a.sv[2], D);
 
+  // sink accumulators: lane l holds key 4(l/16) + i, head-dim column 16 nb + l % 16
+  f32x4 dks[SINK ? NB16 : 1], dvs[SINK ? NB16 : 1];
+  if constexpr (SINK) {
+#pragma unroll
+    for (int nb = 0; nb < NB16; ++nb) {
+      dks[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dvs[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  uint16_t* ptile = SINK ? (D >= 32 ? stash + 2 * TILE : lds + 2 * BUF + 4 * STASH + wave * 1024) : nullptr;
+
   int tile = t_lo + pos;
+  int run_first = tile;  // first tile of the current run of tiles of one (batch, KV head)
   float lse_next = 0.f;
   if (tile < t_hi) {
     const TileIdx t0 = decode(tile);
@@ -136,17 +166,22 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
     const TileIdx t = decode(tile);
     const int qw = t.qw, q = qw + r32;
     const bool wave_active = qw < L;
+    const bool has_next = tile + wgs_x < t_hi;
 
     // Row operands and row statistics, from the stash (this wave's own DMA, complete by now:
     // see the wait after the key loop).  delta = rowsum(dO o O) is stored for the dK/dV kernel;
     // the dP accumulator of every key tile starts from -delta, so dS = P * acc.
+    const uint16_t* Qs = stash;
+    const uint16_t* Ds = stash + TILE;
+    const uint16_t* Os = stash + 2 * TILE;
     u32x4 qf[KS], dof[KS];
     float dsum = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      qf[ks] = lds16(stash + (0 * KS + ks) * 512 + 8 * lane) ^ a.qsign;
-      dof[ks] = lds16(stash + (1 * KS + ks) * 512 + 8 * lane);
-      dsum += dot8<E>(dof[ks], lds16(stash + (2 * KS + ks) * 512 + 8 * lane));
+      const int off = swz_off<D>(r32, hf * (D / 2) + 8 * ks);
+      qf[ks] = lds16(Qs + off) ^ a.qsign;
+      dof[ks] = lds16(Ds + off);
+      dsum += dot8<E>(dof[ks], lds16(Os + off));
     }
     const float delta = sum_halves(dsum);
     const float ndelta = -delta;
@@ -160,6 +195,8 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
       for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m);
       if (lane == 0) a.dsink_part[(int64_t(t.b) * a.Hq + t.hw) * (a.Lp / 32) + qw / 32] = -v;
     }
+    // this wave's rows add to the sink keys' gradients (rows from sink_row0 on)
+    const bool sink_rows = SINK && wave_active && qw + 31 >= a.sink_row0;
 
     f32x16 acc[DB];
 #pragma unroll
@@ -189,6 +226,16 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
         }
       }
     };
+    // the next tile's rows into the stash, once this tile's have been read out of it (and, on
+    // the sink path, after the transposed reads of its Q and dO tiles in key block 0)
+    auto refill = [&]() {
+      if (has_next) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const TileIdx tn = decode(tile + wgs_x);
+        stash_rows(tn);
+        lse_next = load_lse(tn);
+      }
+    };
 
     gload(qplan_block(plan, 0));
     sstore(0);
@@ -198,13 +245,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
       const int kb = qplan_block(plan, i);
       const bool more = i + 1 < plan.nb;
       if (more) gload(qplan_block(plan, i + 1));
-      // the next tile's rows into the stash, once this tile's have been read out of it
-      if (i == 0 && tile + wgs_x < t_hi) {
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        const TileIdx tn = decode(tile + wgs_x);
-        stash_rows(tn);
-        lse_next = load_lse(tn);
-      }
+      if (!SINK && i == 0) refill();
       if (wave_active) {
         const uint16_t* Kl = lds + (i & 1) * BUF;
         const uint16_t* Vl = Kl + BN * D;
@@ -255,20 +296,63 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
           }
           // dQ^T += K^T dS^T: K^T read transposed from the row-major K block, keys in the row
           // order of the dS^T C tile
-          float ds[16];
+          float p[16], ds[16];
 #pragma unroll
-          for (int e = 0; e < 16; ++e) ds[e] = fast_exp2(fmaf(s[e], a.c, -lse2)) * dp[e];
+          for (int e = 0; e < 16; ++e) {
+            p[e] = fast_exp2(fmaf(s[e], a.c, -lse2));
+            ds[e] = p[e] * dp[e];
+          }
           const u32x4 d0 = pack8<E>(ds), d1 = pack8<E>(ds + 8);
 #pragma unroll
           for (int db = 0; db < DB; ++db) {
             acc[db] = E::mfma(tr_frag_swz<D>(Kl, 32 * sb, 32 * db, D), d0, acc[db]);
             acc[db] = E::mfma(tr_frag_swz<D>(Kl, 32 * sb + 16, 32 * db, D), d1, acc[db]);
           }
+          if constexpr (SINK) {
+            if (ks0 == 0 && sink_rows) {
+              // P and dS of keys [0, 16) (registers 0..7: keys 4hf + 0..3 and 8 + 4hf + 0..3 of
+              // row q), rows before sink_row0 zeroed, into the [32 rows][16 keys] tiles
+              const bool row_on = q >= a.sink_row0;
+              float pz[8], dz[8];
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                pz[e] = row_on ? p[e] : 0.f;
+                dz[e] = row_on ? ds[e] : 0.f;
+              }
+              uint16_t* Pt = ptile;
+              uint16_t* St = ptile + 512;
+#pragma unroll
+              for (int j = 0; j < 2; ++j) {
+                const int o = r32 * 16 + 8 * j + 4 * hf;
+                *reinterpret_cast<u32x2*>(Pt + o) = u32x2{E::pack2(pz[4 * j], pz[4 * j + 1]), E::pack2(pz[4 * j + 2], pz[4 * j + 3])};
+                *reinterpret_cast<u32x2*>(St + o) = u32x2{E::pack2(dz[4 * j], dz[4 * j + 1]), E::pack2(dz[4 * j + 2], dz[4 * j + 3])};
+              }
+              // A operands P^T / dS^T (16 keys x 32 rows): lane l gets key l % 16, rows
+              // 8(l/16) + 0..7, by two transposing reads of 4 rows each
+              const int g4 = lane >> 4, i16 = lane & 15;
+              const int pr = (8 * g4 + (i16 >> 2)) * 16 + 4 * (i16 & 3);
+              const u32x2 pa0 = ds_read_tr16(Pt + pr), pa1 = ds_read_tr16(Pt + pr + 64);
+              const u32x2 sa0 = ds_read_tr16(St + pr), sa1 = ds_read_tr16(St + pr + 64);
+              const u32x4 pa = {pa0[0], pa0[1], pa1[0], pa1[1]}, sa = {sa0[0], sa0[1], sa1[0], sa1[1]};
+#pragma unroll
+              for (int nb = 0; nb < NB16; ++nb) {
+                // B operands dO / Q (32 rows x 16 columns): lane l gets column 16 nb + l % 16 of
+                // the same rows, read transposed from the stash tiles
+                const int rr = 8 * g4 + (i16 >> 2), cc = 16 * nb + 4 * (i16 & 3);
+                const u32x2 db0 = ds_read_tr16(Ds + swz_off<D>(rr, cc)), db1 = ds_read_tr16(Ds + swz_off<D>(rr + 4, cc));
+                const u32x2 qb0 = ds_read_tr16(Qs + swz_off<D>(rr, cc)), qb1 = ds_read_tr16(Qs + swz_off<D>(rr + 4, cc));
+                dvs[nb] = E::mfma16(pa, u32x4{db0[0], db0[1], db1[0], db1[1]}, dvs[nb]);
+                dks[nb] = E::mfma16(sa, u32x4{qb0[0], qb0[1], qb1[0], qb1[1]}, dks[nb]);
+              }
+            }
+          }
         }
       }
+      if (SINK && i == 0) refill();
       if (more) sstore((i + 1) & 1);
       __syncthreads();
     }
+    if (plan.nb == 0) refill();  // no key block (cannot happen for valid masks; kept for safety)
     // the next tile's stash has landed (waited here, before this tile's dQ stores, which would
     // otherwise also be waited for)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -285,6 +369,48 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const Args a) {
         const int d0 = 32 * db + (D >= 32 ? 16 * hf : 0);
         st16(dqp + 2 * d0, pack8<E>(v));
         st16(dqp + 2 * (d0 + 8), pack8<E>(v + 8));
+      }
+    }
+
+    if constexpr (SINK) {
+      // Flush at the end of a run of tiles of one (batch, KV head): the waves' accumulators are
+      // summed in LDS (the K/V buffers: every wave has passed the key loop's last barrier, and
+      // the next tile stages K/V only after the barrier below) in wave order and written to the
+      // slot of the run's first tile.  A workgroup has at most one run per (batch, KV head), and
+      // the runs of one XCD start at the first wgs_x tiles of its share of that (batch, KV head),
+      // which is how bwd_sink_fold_kernel finds the slots.
+      const bool flush = !has_next || (tile + wgs_x) / tiles_per_kv != tile / tiles_per_kv;
+      if (flush) {
+        const int sr = a.srows;
+        float* red = reinterpret_cast<float*>(lds);
+        const int g4 = lane >> 4, i16 = lane & 15;
+#pragma unroll
+        for (int nb = 0; nb < NB16; ++nb)
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const int key = 4 * g4 + ii;
+            if (key < sr) {
+              red[((wave * 2 + 0) * sr + key) * D + 16 * nb + i16] = dks[nb][ii];
+              red[((wave * 2 + 1) * sr + key) * D + 16 * nb + i16] = dvs[nb][ii];
+            }
+          }
+        __syncthreads();
+        const int n_out = 2 * sr * D;
+        float* slot = a.dq_sink_part + int64_t(run_first) * n_out;
+        run_first = tile + wgs_x;
+        for (int x = tid; x < n_out; x += 256) {
+          const int kind = x / (sr * D), rest = x % (sr * D);
+          float v = 0.f;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) v += red[(w * 2 + kind) * sr * D + rest];
+          slot[x] = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int nb = 0; nb < NB16; ++nb) {
+          dks[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          dvs[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
     }
   }
@@ -644,9 +770,10 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Sink fold: the dK/dV rows of the chunked sink keys are the sum of the fp32 partials that the
-// dK/dV kernel's regular and chunk workgroups wrote for them.  A separate launch, so the
-// partials of every workgroup are visible without a device-wide fence inside the dK/dV kernel.
+// Sink fold: the dK/dV rows of the split sink keys are the sum of fp32 partials: those the
+// dK/dV kernel's regular and chunk workgroups wrote for them and, in dq_sink_mode, those the dQ
+// kernel flushed (the flagged tiles of the (batch, KV head)).  A separate launch, so every
+// partial is visible without a device-wide fence inside the producing kernels.
 // One workgroup per (b, KV head, sink key): thread (g, d) adds slots g, g + NG, g + 2 NG, ...
 // (their loads in flight together), then the NG group sums are added in order g = 0, 1, ... --
 // a fixed order, so results are deterministic.
@@ -681,6 +808,39 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
     for (int j = 0; j < kBatch; ++j) {
       sk += xk[j];
       sv += xv[j];
+    }
+  }
+  if (a.sink_dq) {
+    // The dQ kernel's flushed partials of this (b, KV head) = tiles [bh tpk, (bh + 1) tpk): on
+    // XCD x, whose tiles are [x_lo, x_hi) and whose a.dq_wgs / 8 workgroups stride through them,
+    // the runs start at the first a.dq_wgs / 8 tiles of [max(x_lo, lo), min(x_hi, hi)).  All the
+    // loads are independent; slots are added in (XCD, tile) order.
+    const int tpk = a.n_qtiles * (a.G / a.wh);
+    const int n_tiles = tpk * a.B * a.Hkv;
+    const int wgs_x = a.dq_wgs / 8;
+    const int lo = bh * tpk, hi = lo + tpk;
+    const int per = n_tiles / 8, rem = n_tiles % 8;
+    const int n_out = 2 * a.srows * D;
+    const float* dsrc = a.dq_sink_part + row * D + d;
+    for (int x = 0; x < 8; ++x) {
+      const int x_lo = x * per + min(x, rem), x_hi = x_lo + per + (x < rem ? 1 : 0);
+      const int A = max(x_lo, lo), B = min(x_hi, hi);
+      const int n = B > A ? min(wgs_x, B - A) : 0;
+      for (int j0 = g; j0 < n; j0 += NG * kBatch) {
+        float xk[kBatch], xv[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int jj = j0 + j * NG;
+          const float* p = dsrc + int64_t(A + (jj < n ? jj : 0)) * n_out;
+          xk[j] = jj < n ? p[0] : 0.f;
+          xv[j] = jj < n ? p[a.srows * D] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          sk += xk[j];
+          sv += xv[j];
+        }
+      }
     }
   }
   part[0][g][d] = sk;
@@ -723,13 +883,14 @@ __global__ __launch_bounds__(256) void bwd_sink_logit_kernel(const Args a) {
 }
 
 // Resident workgroups per CU of a kernel (hipOccupancyMaxActiveBlocksPerMultiprocessor,
-// 256 threads), remembered per kernel: it depends only on the kernel's resources.
-template <typename K>
-static int resident_per_cu(K kernel) {
+// 256 threads), remembered per kernel (one cache per template argument, i.e. per kernel): it
+// depends only on the kernel's resources.
+template <auto Kernel>
+static int resident_per_cu() {
   static int cached = 0;  // benign race: every thread computes the same value
   if (cached == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 256, 0) != hipSuccess || n < 1) n = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, Kernel, 256, 0) != hipSuccess || n < 1) n = 1;
     cached = n;
   }
   return cached;
@@ -743,14 +904,24 @@ static int device_cus() {
   return n;
 }
 
+// Grid of the dQ kernel: one resident wave of workgroups, a multiple of the 8 XCDs (the sink
+// fold recomputes it to find the dQ kernel's sink slots).
+template <typename E, int D, bool SINK>
+static int dq_grid(const Args& a) {
+  const int n_tiles = a.n_qtiles * (a.B * a.Hq / a.wh);
+  const int slots = resident_per_cu<bwd_dq_kernel<E, D, SINK>>() * device_cus();
+  return 8 * ((min(n_tiles, slots) + 7) / 8);
+}
+
+template <typename E, int D, bool SINK>
+static hipError_t launch_dq_s(const Args& a, hipStream_t stream) {
+  hipLaunchKernelGGL((bwd_dq_kernel<E, D, SINK>), dim3(dq_grid<E, D, SINK>(a)), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
 template <typename E, int D>
 static hipError_t launch_dq_d(const Args& a, int, hipStream_t stream) {
-  const int n_tiles = a.n_qtiles * (a.B * a.Hq / a.wh);
-  // one resident wave of workgroups, a multiple of the 8 XCDs
-  const int slots = resident_per_cu(bwd_dq_kernel<E, D>) * device_cus();
-  const int wgs = 8 * ((min(n_tiles, slots) + 7) / 8);
-  hipLaunchKernelGGL((bwd_dq_kernel<E, D>), dim3(wgs), dim3(256), 0, stream, a);
-  return hipGetLastError();
+  return a.sink_dq ? launch_dq_s<E, D, true>(a, stream) : launch_dq_s<E, D, false>(a, stream);
 }
 
 template <typename E, int D>
@@ -760,7 +931,9 @@ static hipError_t launch_dkdv_d(const Args& a, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.nsp == 0) return e;
   const int64_t n = int64_t(a.B) * a.Hkv * min(a.S, kKvKeys * a.nsp);  // one workgroup per sink key
-  hipLaunchKernelGGL((bwd_sink_fold_kernel<E, D>), dim3(unsigned(n)), block, 0, stream, a);
+  Args af = a;
+  if (a.sink_dq) af.dq_wgs = dq_grid<E, D, true>(a);
+  hipLaunchKernelGGL((bwd_sink_fold_kernel<E, D>), dim3(unsigned(n)), block, 0, stream, af);
   return hipGetLastError();
 }
 

@@ -71,17 +71,28 @@ void choose_qmajor(int G, int hmax, int* hpw, int* wh, int* wq) {
 
 struct SinkPlan {
   int nsp, n_chunks, srows;  // chunked blocks, chunks per block, stored sink rows per block
+  int dq;                    // sink rows past block 0's window go through the dQ kernel
 };
 
 SinkPlan sink_plan(int L, int W, int S) {
   // clamp as the kernels do
   W = W < 0 ? 0 : (W > L ? L : W);
   S = S < 0 ? 0 : (S > L ? L : S);
-  SinkPlan p{0, 0, 0};
+  SinkPlan p{0, 0, 0, 0};
   p.nsp = fa::kv_sink_blocks(L, W, S);
-  p.n_chunks = fa::kv_n_chunks(L, W, S, kChunkRows);
+  p.dq = fa::dq_sink_mode(L, W, S) ? 1 : 0;
+  p.n_chunks = p.dq ? 0 : fa::kv_n_chunks(L, W, S, kChunkRows);
   p.srows = S < fa::kKvKeys ? S : fa::kKvKeys;
   return p;
+}
+
+// Tiles of the dQ kernel: row tiles of 32 * wq rows times head groups of wh heads (one query
+// head per wave).
+int64_t dq_tiles(int B, int Hq, int Hkv, int L) {
+  int hpw, wh, wq;
+  choose_qmajor(Hq / Hkv, 1, &hpw, &wh, &wq);
+  const int64_t n_qtiles = (int64_t(L) + 32 * wq - 1) / (32 * wq);
+  return n_qtiles * B * (Hq / wh);
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -97,6 +108,12 @@ size_t delta_bytes(int B, int Hq, int L) {
 // fp32 partial sums of the sink rows: [B * Hkv][nsp][n_chunks + 1 slots][dK, dV][srows][D]
 size_t partial_bytes(int B, int Hkv, int D, const SinkPlan& sp) {
   return align256(size_t(B) * Hkv * sp.nsp * (sp.n_chunks + 1) * 2 * sp.srows * D * sizeof(float));
+}
+
+// dq_sink_mode: the dQ kernel's flushed sink partials, [n_tiles][dK, dV][srows][D] fp32 (a slot
+// per tile; a run of tiles writes the slot of its first tile)
+size_t dq_sink_slot_bytes(int B, int Hq, int Hkv, int L, int D, const SinkPlan& sp) {
+  return sp.dq ? align256(size_t(dq_tiles(B, Hq, Hkv, L)) * 2 * sp.srows * D * sizeof(float)) : 0;
 }
 
 void copy3(int64_t dst[3], const int64_t src[3]) {
@@ -218,7 +235,7 @@ size_t fa_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t heads_kv, 
     return 0;
   const SinkPlan sp = sink_plan(seqlen, window, sink);
   return delta_bytes(batch, heads_q, seqlen) + partial_bytes(batch, heads_kv, head_dim, sp) +
-         dsink_part_bytes(batch, heads_q, seqlen);
+         dsink_part_bytes(batch, heads_q, seqlen) + dq_sink_slot_bytes(batch, heads_q, heads_kv, seqlen, head_dim, sp);
 }
 
 }  // extern "C"
@@ -264,8 +281,12 @@ int prepare_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
   const SinkPlan sp = sink_plan(a.L, p->window, p->sink);
   char* ws = static_cast<char*>(workspace);
   a.partial = reinterpret_cast<float*>(ws + delta_bytes(a.B, a.Hq, a.L));
-  a.dsink_part = reinterpret_cast<float*>(ws + delta_bytes(a.B, a.Hq, a.L) +
-                                          partial_bytes(a.B, a.Hkv, p->head_dim, sp));
+  const size_t off_dsink = delta_bytes(a.B, a.Hq, a.L) + partial_bytes(a.B, a.Hkv, p->head_dim, sp);
+  a.dsink_part = reinterpret_cast<float*>(ws + off_dsink);
+  const size_t off_dq_slots = off_dsink + dsink_part_bytes(a.B, a.Hq, a.L);
+  a.sink_dq = sp.dq;
+  a.sink_row0 = fa::dq_sink_row0(a.L, a.W);
+  if (sp.dq) a.dq_sink_part = reinterpret_cast<float*>(ws + off_dq_slots);
   a.n_kblocks = (a.L + fa::kKvKeys - 1) / fa::kKvKeys;
   a.nsp = sp.nsp;
   a.n_chunks = sp.n_chunks;

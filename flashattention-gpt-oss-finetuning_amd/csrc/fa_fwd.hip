@@ -326,12 +326,12 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
 
 // Resident workgroups per CU of a kernel, remembered per kernel (it depends only on the
 // kernel's resources).
-template <typename K>
-static int fwd_resident_per_cu(K kernel) {
+template <auto Kernel>
+static int fwd_resident_per_cu() {
   static int cached = 0;  // benign race: every thread computes the same value
   if (cached == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 256, 0) != hipSuccess || n < 1) n = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, Kernel, 256, 0) != hipSuccess || n < 1) n = 1;
     cached = n;
   }
   return cached;
@@ -345,7 +345,7 @@ static hipError_t launch_fwd_h(const Args& a, hipStream_t stream) {
       cus < 1)
     cus = 256;
   // one resident wave of workgroups, a multiple of the 8 XCDs
-  const int slots = fwd_resident_per_cu(fwd_kernel<E, D, HPW>) * cus;
+  const int slots = fwd_resident_per_cu<fwd_kernel<E, D, HPW>>() * cus;
   const int wgs = 8 * ((min(n_tiles, slots) + 7) / 8);
   hipLaunchKernelGGL((fwd_kernel<E, D, HPW>), dim3(wgs), dim3(256), 0, stream, a);
   return hipGetLastError();

@@ -108,4 +108,15 @@ FA_HD int kv_n_chunks(int L, int W, int S, int chunk_rows) {
   return kv_sink_blocks(L, W, S) > 0 ? (L - kv_chunk_base(0, L, W) + chunk_rows - 1) / chunk_rows : 0;
 }
 
+// ---- sink rows in the dQ kernel ------------------------------------------------------------------
+// With at most kDqSinkKeys sink keys (all in key block 0) and rows past block 0's window, the dQ
+// kernel -- which visits keys [0, 32) for every query tile -- also accumulates the sink keys' dK/dV
+// contributions of those rows, [dq_sink_row0, L); the key-major kernel then runs no chunk
+// workgroups and covers only rows [0, dq_sink_row0) of block 0.
+constexpr int kDqSinkKeys = 16;
+
+FA_HD bool dq_sink_mode(int L, int W, int S) { return S >= 1 && S <= kDqSinkKeys && kv_sink_blocks(L, W, S) == 1; }
+
+FA_HD int dq_sink_row0(int L, int W) { return kv_window_end(0, L, W); }
+
 }  // namespace fa

@@ -101,9 +101,30 @@ static int check_kvmajor(int L, int W, int S, int chunk_rows) {
   };
   for (int kblk = 0; kblk < nkb; ++kblk)
     if (sweep(kblk, kKvKeys * kblk, kv_window_end(kblk, L, W), false)) return 1;
-  for (int kblk = 0; kblk < nsp; ++kblk)
-    for (int c = 0; c < n_chunks; ++c)
-      if (sweep(kblk, kv_chunk_lo(kblk, c, chunk_rows, L, W), kv_chunk_hi(kblk, c, chunk_rows, L, W), true)) return 1;
+  if (dq_sink_mode(L, W, S)) {
+    // the dQ kernel's sink rows: every query tile of wq 32-row waves visits keys [0, 32) through
+    // its plan; rows >= dq_sink_row0 add keys [0, kDqSinkKeys) where allowed, keys < S counted
+    if (S > kDqSinkKeys || nsp != 1) return fail("dq sink mode with too many sink keys", L, W, S, chunk_rows, 0, 0, nsp);
+    const int row0 = dq_sink_row0(L, W);
+    for (int wq : {1, 2, 4})
+      for (int q0 = 0; q0 < L; q0 += 32 * wq) {
+        const QPlan p = qplan(q0, 32 * wq, L, W, S);
+        const bool visits0 = p.nb > 0 && qplan_block(p, 0) == 0;
+        for (int w = 0; w < wq; ++w) {
+          const int qw = q0 + 32 * w;
+          if (qw >= L || qw + 31 < row0) continue;
+          if (!visits0 || !wave_needs(0, qw, L, W, S)) return fail("dq sink tile misses key block 0", L, W, S, wq, qw, 0, 0);
+          if (wq != 1) continue;  // count once
+          for (int q = qw; q < qw + 32 && q < L; ++q)
+            for (int k = 0; k < S; ++k)
+              if (q >= row0 && allowed(q - k, k, W, S)) ++cnt[size_t(q) * L + k];
+        }
+      }
+  } else {
+    for (int kblk = 0; kblk < nsp; ++kblk)
+      for (int c = 0; c < n_chunks; ++c)
+        if (sweep(kblk, kv_chunk_lo(kblk, c, chunk_rows, L, W), kv_chunk_hi(kblk, c, chunk_rows, L, W), true)) return 1;
+  }
   for (int q = 0; q < L; ++q)
     for (int k = 0; k < L; ++k) {
       const int want = ref_allowed(q, k, W, S) ? 1 : 0;

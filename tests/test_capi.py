@@ -211,14 +211,20 @@ def test_workspace_bytes():
     # the window of the sink block; the learned-sink partials: B*Hq*ceil(L/32) floats, 256-aligned
     assert ws(1, 8, 2, 128, 64, 200, 4) == 8 * 128 * 4 + 256
     assert ws(1, 8, 2, 100, 64, 200, 4) == 8 * 128 * 4 + 256
-    # sink split: 1 block of 64 keys; its window ends at row 191, chunks of 64 rows start at 160
-    # (rounded down to 32): ceil((4096 - 160) / 64) = 62 chunks + the regular slot, dK and dV,
-    # S = 4 sink rows x D fp32 each
     L_, D = 4096, 64
     expect_delta = 64 * 4096 * 4
-    expect_partial = 8 * 1 * (62 + 1) * 2 * 4 * D * 4
     expect_dsink = 64 * (4096 // 32) * 4
-    assert ws(1, 64, 8, L_, D, 128, 4) == expect_delta + expect_partial + expect_dsink
+    # S <= 16 sink keys, rows past block 0's window (row 191): the dK/dV kernel keeps one slot
+    # (block 0's own rows) per KV head, dK and dV, S = 4 rows x D fp32; the dQ kernel's slots are
+    # one per tile -- 4096 / 32 row tiles x 64 / 4 head groups
+    expect_partial = 8 * 1 * 1 * 2 * 4 * D * 4
+    expect_dq = 128 * 16 * 2 * 4 * D * 4
+    assert ws(1, 64, 8, L_, D, 128, 4) == expect_delta + expect_partial + expect_dsink + expect_dq
+    # S > 16: the sink rows are split into chunk workgroups of the dK/dV kernel: block 0's window
+    # ends at row 191, chunks of 64 rows start at 160 (rounded down to 32):
+    # ceil((4096 - 160) / 64) = 62 chunks + the regular slot, S = 40 sink rows
+    expect_partial = 8 * 1 * (62 + 1) * 2 * 40 * D * 4
+    assert ws(1, 64, 8, L_, D, 128, 40) == expect_delta + expect_partial + expect_dsink
     # invalid problems give 0
     assert ws(1, 8, 3, 128, 64, 16, 4) == 0
     assert ws(1, 8, 2, 128, 64, 0, 0) == 0

@@ -119,7 +119,13 @@ EDGE_CASES = [
     pytest.param(1, 4, 2, 300, 32, 64, 4, FP, id="E9-D32"),
     pytest.param(1, 4, 2, 300, 128, 64, 4, BF, id="E9-D128-bf16"),
     pytest.param(1, 8, 1, 300, 128, 64, 20, FP, id="E9-D128-fp16-G8"),
-    pytest.param(1, 8, 2, 1000, 64, 16, 4, BF, id="sink-chunks"),
+    pytest.param(1, 8, 2, 1000, 64, 16, 4, BF, id="dq-sinks"),
+    pytest.param(1, 4, 4, 700, 16, 40, 3, FP, id="dq-sinks-D16-G1"),
+    pytest.param(1, 8, 2, 900, 32, 100, 16, BF, id="dq-sinks-D32-S16"),
+    pytest.param(1, 8, 1, 600, 128, 50, 7, BF, id="dq-sinks-D128-G8"),
+    pytest.param(2, 6, 2, 500, 64, 20, 9, FP, id="dq-sinks-G3-B2"),
+    pytest.param(1, 4, 2, 200, 64, 136, 2, BF, id="dq-sinks-one-row"),
+    pytest.param(8, 64, 64, 200, 32, 10, 2, BF, id="dq-sinks-many-groups"),
     pytest.param(1, 8, 2, 1100, 64, 8, 40, FP, id="sink-chunks-two-blocks"),
     pytest.param(1, 4, 1, 700, 16, 7, 70, BF, id="sink-chunks-D16"),
     pytest.param(1, 4, 2, 700, 128, 30, 33, BF, id="sink-chunks-D128"),
