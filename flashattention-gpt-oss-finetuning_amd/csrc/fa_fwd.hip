@@ -26,6 +26,146 @@ namespace fa {
 
 constexpr float kRescaleGap = 8.f;  // log2 units: P stays <= 256 between rescales
 
+// One 32-key half [ks0, ks0 + 32) of the keys -- swizzled [32][D] K and V tiles in LDS at Kl, Vl --
+// for the HPW heads of a wave whose 32 rows start at qw (this lane's row q): masked scores, the
+// online-softmax update of (m2, lsum, acc) and O^T += V^T P^T.
+// Additive masks of the partially masked halves that recur on every tile, built once per
+// workgroup in LDS (fwd_patterns): lane l's 16 values at [(e / 4) * 64 + l] * 4 + e % 4 of pattern
+// p = 0 (the diagonal half, qw - ks0 = 0), 1 and 2 (the window-edge halves, qw - ks0 = e1 and
+// e1 + 32, both multiples of 32 in [W - 31, W + 30]) and 3 (keys [0, 32) seen only as sinks).
+constexpr int kPatterns = 4;
+constexpr int kPatternFloats = 16 * 64;
+
+struct EdgeOffsets {
+  int e1, e2;  // qw - ks0 of the window-edge halves, -1 where there is none
+};
+
+__device__ __forceinline__ EdgeOffsets edge_offsets(int W) {
+  EdgeOffsets r{-1, -1};
+  if (W > 31) {
+    r.e1 = (W - 31 + 31) / 32 * 32;
+    r.e2 = r.e1 + 32 <= W + 30 ? r.e1 + 32 : -1;
+  }
+  return r;
+}
+
+// Wave p of the workgroup writes pattern p (call with 4 waves, before the first barrier).
+__device__ __forceinline__ void fwd_patterns(float* pat, int W, int S) {
+  const int lane = threadIdx.x & 63, p = threadIdx.x >> 6;
+  const int r32 = lane & 31, hf = lane >> 5;
+  const EdgeOffsets eo = edge_offsets(W);
+  const int dl = p == 1 ? eo.e1 : p == 2 ? eo.e2 : 0;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int off = 8 * (e / 4) + (e % 4);
+    const int d = r32 - 4 * hf - off;  // q - k on the diagonal half
+    const bool ok = p == 3 ? 4 * hf + off < S : unsigned(d + dl) < unsigned(W);
+    pat[p * kPatternFloats + ((e >> 2) * 64 + lane) * 4 + (e & 3)] = ok ? 0.f : kNegInf;
+  }
+}
+
+template <typename E, int D, int HPW>
+__device__ __forceinline__ void fwd_half(const Args& a, const uint16_t* Kl, const uint16_t* Vl, int ks0, int qw, int q,
+                                         const u32x4 (&qf)[HPW][D / 16], float (&m2)[HPW], float (&lsum)[HPW],
+                                         f32x16 (&acc)[HPW][D >= 32 ? D / 32 : 1], const float* pat,
+                                         EdgeOffsets eo) {
+  constexpr int KS = D / 16;
+  constexpr int DB = D >= 32 ? D / 32 : 1;
+  const int lane = threadIdx.x & 63;
+  const int r32 = lane & 31, hf = lane >> 5;
+  const int W = a.W, S = a.S;
+  // S^T = K Q^T for every head of the wave (the K fragments are shared).  Masked tiles start
+  // the accumulator from an additive bias, 0 (allowed) or -inf (masked), shared by the
+  // heads.  Register e of this lane holds key ks0 + 4hf + off(e), off(e) = 8(e/4) + e%4,
+  // of row q; with dq0 = q - ks0 - 4hf the test is one unsigned compare,
+  // allowed = (dq0 - off) < lim, lim = W for ordinary keys and 2^31 for sink keys (any
+  // q >= k).  Which form applies is wave-uniform.
+  f32x16 s[HPW];
+  // Head by head: head 0's scores are complete while head 1's MFMAs are still in the
+  // pipe, and head 0's softmax (VALU) overlaps them.
+  u32x4 kf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    kf[ks] = *reinterpret_cast<const u32x4*>(Kl + swz_off<D>(r32, hf * (D / 2) + 8 * ks));
+  auto qk = [&](const f32x16& c0) {
+#pragma unroll
+    for (int h = 0; h < HPW; ++h)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) s[h] = E::mfma(kf[ks], qf[h][ks], ks == 0 ? c0 : s[h]);
+  };
+  if (tile_full(ks0, qw, W, S)) {
+    qk(f32x16{});
+  } else {
+    f32x16 bias;
+    const int dl = qw - ks0;
+    const int pi = ks0 >= S ? (dl == 0 ? 0 : dl == eo.e1 ? 1 : dl == eo.e2 ? 2 : -1)
+                            : (ks0 == 0 && S < 32 && qw - 31 >= W ? 3 : -1);
+    const int dq0 = q - ks0 - 4 * hf;
+    if (pi >= 0) {  // a recurring pattern: four 16-byte LDS reads
+      const f32x4* p4 = reinterpret_cast<const f32x4*>(pat + pi * kPatternFloats) + lane;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 v = p4[64 * j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bias[4 * j + i] = v[i];
+      }
+    } else if (ks0 >= S || ks0 + 32 <= S) {  // one limit for all 32 keys
+      const unsigned lim = ks0 >= S ? unsigned(W) : 0x80000000u;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        bias[e] = unsigned(dq0 - (8 * (e / 4) + (e % 4))) < lim ? 0.f : kNegInf;
+    } else {  // the sink boundary S falls inside these keys
+      const int sl = S - ks0 - 4 * hf;  // keys with off < sl are sinks
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int off = 8 * (e / 4) + (e % 4);
+        bias[e] = unsigned(dq0 - off) < (off < sl ? 0x80000000u : unsigned(W)) ? 0.f : kNegInf;
+      }
+    }
+    qk(bias);
+  }
+  // V^T operands of O^T += V^T P^T, shared by the heads: read transposed from the
+  // row-major V block, keys in the row order of the P^T C tile.
+  u32x4 vf[DB][2];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) vf[db][t] = tr_frag_swz<D>(Vl, 16 * t, 32 * db, D);
+#pragma unroll
+  for (int h = 0; h < HPW; ++h) {
+    float m = s[h][0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) m = fmaxf(m, s[h][e]);
+    const float mx = max_halves(m) * a.c;  // row max in the log2 domain (-inf stays -inf)
+    // Lazy rescaling: the exponent reference m2 moves only when some row's maximum
+    // exceeds it by more than kRescaleGap, so P <= 2^kRescaleGap and the rescale of the
+    // accumulators is skipped on most steps.  Results are the same up to rounding.
+    if (wave_any(mx > m2[h] + kRescaleGap)) {
+      const float mnew = fmaxf(m2[h], mx);
+      const float alpha = mnew == kNegInf ? 1.f : fast_exp2(m2[h] - mnew);
+      m2[h] = mnew;
+      lsum[h] *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[h][db] *= alpha;
+    }
+    const float ms = m2[h] == kNegInf ? 0.f : m2[h];
+    float sv[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sv[e] = fast_exp2(fmaf(s[h][e], a.c, -ms));
+    const u32x4 pb0 = pack8<E>(sv), pb1 = pack8<E>(sv + 8);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      acc[h][db] = E::mfma(vf[db][0], pb0, acc[h][db]);
+      acc[h][db] = E::mfma(vf[db][1], pb1, acc[h][db]);
+    }
+    // the row sum adds the 16-bit P that the PV product uses
+#pragma unroll
+    for (int w = 0; w < 4; ++w) lsum[h] = E::sum2(pb0[w], lsum[h]);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) lsum[h] = E::sum2(pb1[w], lsum[h]);
+  }
+}
+
 template <typename E, int D, int HPW>
 __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   constexpr int BN = 64;                   // keys per LDS block
@@ -40,7 +180,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // workgroup per CU needs.
   constexpr bool kStash = D <= 64;
   constexpr int STASH = kStash ? HPW * KS * 512 : 0;  // per wave: the next tile's Q fragments
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF + 4 * STASH];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF + 4 * STASH + 2 * kPatterns * kPatternFloats];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -104,6 +244,11 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   const int off_l0 = swz_off<D>(row0, 8 * col0);
   const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
   const uint32_t nk_bytes = span_bytes(L, a.sk[2], D), nv_bytes = span_bytes(L, a.sv[2], D);
+
+  // the recurring masks (made visible by the barrier before the first key block)
+  float* const pat = reinterpret_cast<float*>(lds + 2 * BUF + 4 * STASH);
+  fwd_patterns(pat, W, S);
+  const EdgeOffsets eo = edge_offsets(W);
 
   int tile = t_lo + pos;
   if (kStash && tile < t_hi) {
@@ -196,85 +341,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
       for (int sb = 0; sb < 2; ++sb) {
         const int ks0 = kb + 32 * sb;
         if (!wave_needs(ks0, qw, L, W, S)) continue;
-        // S^T = K Q^T for every head of the wave (the K fragments are shared).  Masked tiles start
-        // the accumulator from an additive bias, 0 (allowed) or -inf (masked), shared by the
-        // heads.  Register e of this lane holds key ks0 + 4hf + off(e), off(e) = 8(e/4) + e%4,
-        // of row q; with dq0 = q - ks0 - 4hf the test is one unsigned compare,
-        // allowed = (dq0 - off) < lim, lim = W for ordinary keys and 2^31 for sink keys (any
-        // q >= k).  Which form applies is wave-uniform.
-        f32x16 s[HPW];
-        // Head by head: head 0's scores are complete while head 1's MFMAs are still in the
-        // pipe, and head 0's softmax (VALU) overlaps them.
-        u32x4 kf[KS];
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          kf[ks] = *reinterpret_cast<const u32x4*>(Kl + swz_off<D>(32 * sb + r32, hf * (D / 2) + 8 * ks));
-        auto qk = [&](const f32x16& c0) {
-#pragma unroll
-          for (int h = 0; h < HPW; ++h)
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) s[h] = E::mfma(kf[ks], qf[h][ks], ks == 0 ? c0 : s[h]);
-        };
-        if (tile_full(ks0, qw, W, S)) {
-          qk(f32x16{});
-        } else {
-          f32x16 bias;
-          const int dq0 = q - ks0 - 4 * hf;
-          if (ks0 >= S || ks0 + 32 <= S) {  // one limit for all 32 keys
-            const unsigned lim = ks0 >= S ? unsigned(W) : 0x80000000u;
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-              bias[e] = unsigned(dq0 - (8 * (e / 4) + (e % 4))) < lim ? 0.f : kNegInf;
-          } else {  // the sink boundary S falls inside these keys
-            const int sl = S - ks0 - 4 * hf;  // keys with off < sl are sinks
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              const int off = 8 * (e / 4) + (e % 4);
-              bias[e] = unsigned(dq0 - off) < (off < sl ? 0x80000000u : unsigned(W)) ? 0.f : kNegInf;
-            }
-          }
-          qk(bias);
-        }
-        // V^T operands of O^T += V^T P^T, shared by the heads: read transposed from the
-        // row-major V block, keys in the row order of the P^T C tile.
-        u32x4 vf[DB][2];
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int t = 0; t < 2; ++t) vf[db][t] = tr_frag_swz<D>(Vl, 32 * sb + 16 * t, 32 * db, D);
-#pragma unroll
-        for (int h = 0; h < HPW; ++h) {
-          float m = s[h][0];
-#pragma unroll
-          for (int e = 1; e < 16; ++e) m = fmaxf(m, s[h][e]);
-          const float mx = max_halves(m) * a.c;  // row max in the log2 domain (-inf stays -inf)
-          // Lazy rescaling: the exponent reference m2 moves only when some row's maximum
-          // exceeds it by more than kRescaleGap, so P <= 2^kRescaleGap and the rescale of the
-          // accumulators is skipped on most steps.  Results are the same up to rounding.
-          if (wave_any(mx > m2[h] + kRescaleGap)) {
-            const float mnew = fmaxf(m2[h], mx);
-            const float alpha = mnew == kNegInf ? 1.f : fast_exp2(m2[h] - mnew);
-            m2[h] = mnew;
-            lsum[h] *= alpha;
-#pragma unroll
-            for (int db = 0; db < DB; ++db) acc[h][db] *= alpha;
-          }
-          const float ms = m2[h] == kNegInf ? 0.f : m2[h];
-          float sv[16];
-#pragma unroll
-          for (int e = 0; e < 16; ++e) sv[e] = fast_exp2(fmaf(s[h][e], a.c, -ms));
-          const u32x4 pb0 = pack8<E>(sv), pb1 = pack8<E>(sv + 8);
-#pragma unroll
-          for (int db = 0; db < DB; ++db) {
-            acc[h][db] = E::mfma(vf[db][0], pb0, acc[h][db]);
-            acc[h][db] = E::mfma(vf[db][1], pb1, acc[h][db]);
-          }
-          // the row sum adds the 16-bit P that the PV product uses
-#pragma unroll
-          for (int w = 0; w < 4; ++w) lsum[h] = E::sum2(pb0[w], lsum[h]);
-#pragma unroll
-          for (int w = 0; w < 4; ++w) lsum[h] = E::sum2(pb1[w], lsum[h]);
-        }
+        fwd_half<E, D, HPW>(a, Kl + 32 * sb * D, Vl + 32 * sb * D, ks0, qw, q, qf, m2, lsum, acc, pat, eo);
       }
     }
     if (more) sstore((i + 1) & 1);

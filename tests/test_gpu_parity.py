@@ -119,6 +119,14 @@ EDGE_CASES = [
     pytest.param(1, 4, 2, 300, 32, 64, 4, FP, id="E9-D32"),
     pytest.param(1, 4, 2, 300, 128, 64, 4, BF, id="E9-D128-bf16"),
     pytest.param(1, 8, 1, 300, 128, 64, 20, FP, id="E9-D128-fp16-G8"),
+    pytest.param(1, 16, 2, 1000, 64, 128, 4, BF, id="g8-W128"),
+    pytest.param(2, 16, 2, 777, 64, 129, 0, FP, id="g8-W129-B2"),
+    pytest.param(1, 8, 1, 600, 64, 1, 32, BF, id="g8-W1-S32"),
+    pytest.param(1, 8, 1, 500, 64, 33, 31, FP, id="g8-W33-S31"),
+    pytest.param(1, 16, 1, 300, 64, 100, 1, BF, id="g8-G16-W100"),
+    pytest.param(1, 8, 1, 129, 64, 96, 4, BF, id="g8-short"),
+    pytest.param(1, 8, 1, 2000, 32, 193, 8, FP, id="g8-D32-W193"),
+    pytest.param(1, 8, 1, 700, 32, 64, 0, BF, id="g8-D32-W64"),
     pytest.param(1, 8, 2, 1000, 64, 16, 4, BF, id="dq-sinks"),
     pytest.param(1, 4, 4, 700, 16, 40, 3, FP, id="dq-sinks-D16-G1"),
     pytest.param(1, 8, 2, 900, 32, 100, 16, BF, id="dq-sinks-D32-S16"),
