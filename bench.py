@@ -18,6 +18,7 @@ same way.  Prints ONE JSON line.
                in profiles/<config>_hbm_traffic.txt (null without one)
   cpu_baseline the reference's naive PyTorch path (oracle/naive.py, in the config dtype) timed
                on the host cores on a bounded sample (whole KV groups of the same workload)
+  sdpa_baseline the reference's other baseline, torch SDPA with a boolean mask, on the GPU
 """
 from __future__ import annotations
 
@@ -223,6 +224,49 @@ def time_steps(fa, cfg, q, k, v, do, steps, warmup):
     return dict(fwdbwd_ms=fb_ms, fwdbwd_event_ms=fb_event_ms, fwd_ms=f_ms, bwd_ms=b_ms, peak_mem_gb=peak_gb)
 
 
+def sdpa_baseline(cfg, q, k, v, do, steps=10, warmup=3):
+    """PyTorch-ROCm SDPA with a boolean mask, the reference's second baseline
+    (pytorch_sdpa_attention, benchmark_backward_speed.py:57-65), fwd + autograd bwd on the GPU in
+    the config dtype, timed with HIP events.  On this ROCm build scaled_dot_product_attention has
+    no fused kernel for enable_gqa=True (it would fall back to the math path), so K/V are repeated
+    to Hq heads inside the timed step (as the reference's repeat_kv does) and SDPA is held to the
+    memory-efficient backend: it raises rather than fall back."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    flops_mod = _mod("flops")
+    B, Hq, Hkv, L, D, W, S = (cfg[x] for x in ("B", "Hq", "Hkv", "L", "D", "W", "S"))
+    G = Hq // Hkv
+    pos = torch.arange(L, device=q.device)
+    mask = (pos[None, :] <= pos[:, None]) & (((pos[:, None] - pos[None, :]) < W) | (pos[None, :] < S))
+    qg, kg, vg = (t.detach().clone().requires_grad_() for t in (q, k, v))
+
+    def step():
+        qg.grad = kg.grad = vg.grad = None
+        with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION]):
+            o = F.scaled_dot_product_attention(qg, kg.repeat_interleave(G, 1), vg.repeat_interleave(G, 1),
+                                               attn_mask=mask)
+            o.backward(do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    wl = flops_mod.Workload(B, Hq, Hkv, L, D, W, S)
+    return {"value": round(wl.flops("fwdbwd") / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+            "peak_mem_gb": round(torch.cuda.max_memory_allocated() / 2 ** 30, 3),
+            "backend": "torch SDPA, memory-efficient kernel, boolean [L, L] mask, K/V repeated to Hq heads",
+            "steps": steps, "dtype": cfg["dtype"]}
+
+
 def cpu_baseline(cfg, budget_s):
     """The reference's naive path (benchmark_backward_speed.py:68-85, restated in oracle/naive.py)
     in the config dtype on the host cores, forward + autograd backward, on whole KV groups of the
@@ -241,22 +285,28 @@ def cpu_baseline(cfg, budget_s):
     qw = q[:1, :1, :256].clone().requires_grad_()
     ow = naive.naive_attention(qw, k[:1, :1, :256], v[:1, :1, :256], W, S)
     ow.backward(do[:1, :1, :256])
+    # whole passes over every KV group while the budget lasts (at least one group); a pass that
+    # the budget cuts short still counts its finished groups
     groups = 0
+    passes = 0
     t0 = time.perf_counter()
     elapsed = 0.0
-    for b in range(B):
-        for g in range(Hkv):
-            qs = q[b:b + 1, g * G:(g + 1) * G].clone().requires_grad_()
-            ks = k[b:b + 1, g:g + 1].clone().requires_grad_()
-            vs = v[b:b + 1, g:g + 1].clone().requires_grad_()
-            o = naive.naive_attention(qs, ks, vs, W, S)
-            o.backward(do[b:b + 1, g * G:(g + 1) * G])
-            groups += 1
-            elapsed = time.perf_counter() - t0
+    while elapsed < budget_s:
+        for b in range(B):
+            for g in range(Hkv):
+                qs = q[b:b + 1, g * G:(g + 1) * G].clone().requires_grad_()
+                ks = k[b:b + 1, g:g + 1].clone().requires_grad_()
+                vs = v[b:b + 1, g:g + 1].clone().requires_grad_()
+                o = naive.naive_attention(qs, ks, vs, W, S)
+                o.backward(do[b:b + 1, g * G:(g + 1) * G])
+                groups += 1
+                elapsed = time.perf_counter() - t0
+                if elapsed >= budget_s:
+                    break
             if elapsed >= budget_s:
                 break
-        if elapsed >= budget_s:
-            break
+        else:
+            passes += 1
     pairs = flops_mod.allowed_pairs_per_head(L, W, S)
     flops = 14.0 * D * pairs * groups * G
     total_groups = B * Hkv
@@ -265,9 +315,10 @@ def cpu_baseline(cfg, budget_s):
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{groups} of {total_groups} KV groups ({groups * G} of {B * Hq} query heads) of the same "
-                  f"workload, fwd+bwd of the naive path in {cfg['dtype']} (dense scores, fp32 softmax, autograd), "
-                  f"{elapsed:.1f} s; full-workload estimate {elapsed * total_groups / groups * 1e3:.0f} ms",
+        "sample": f"{groups} KV-group passes ({passes} full passes over the {total_groups} KV groups of the same "
+                  f"workload, {groups * G} query-head passes), fwd+bwd of the naive path in {cfg['dtype']} (dense "
+                  f"scores, fp32 softmax, autograd), {elapsed:.1f} s; full-workload estimate "
+                  f"{elapsed * total_groups / groups * 1e3:.0f} ms",
         "ms_full_workload_est": elapsed * total_groups / groups * 1e3,
         "cpu": platform.processor() or platform.machine(),
         "logical_cores": os.cpu_count(),
@@ -284,6 +335,7 @@ def main():
     ap.add_argument("--kernel-iters", type=int, default=50)
     ap.add_argument("--cpu-baseline-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sdpa-baseline", action="store_true")
     ap.add_argument("--table", action="store_true", help="also time every BASELINE config (stderr)")
     ap.add_argument("--profile-launches", type=int, default=0, metavar="N",
                     help="only launch a 256 MiB copy and each kernel N times (for rocprofv3 --pmc runs)")
@@ -357,6 +409,8 @@ def main():
         "kernels": kernels,
         "roofline": roofline,
     }
+    if not args.no_sdpa_baseline:
+        line["sdpa_baseline"] = sdpa_baseline(cfg, q, k, v, do)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_baseline_seconds)
     if args.table:
