@@ -5,6 +5,10 @@ Public surface (drop-in for flash_attention_gpt_oss.py:340-438):
     flash_swda_with_sink(q, k, v, window_size, sink_size=0, is_causal=True, scale=None)
     swa_sink_attention(q, k, v, window_size, sink_size)      # benchmark registry form
 
+Variable-length (packed) batches, q [total, Hq, D] with cu_seqlens [B + 1]:
+    flash_swda_with_sink_varlen(q, k, v, cu_seqlens, max_seqlen, window_size, sink_size=0,
+                                scale=None, sinks=None)
+
 GPT-OSS integration (gpt_oss.py): learned per-head sink logits, [B, L, H, D] tensors, full and
 sliding layers, and transformers' attention-function interface:
     attention(q, k, v, window_size=None, sink_size=0, sinks=None, scale=None, layout="bhld")
@@ -14,8 +18,8 @@ sliding layers, and transformers' attention-function interface:
 The directory name is not a Python identifier; import it with
 ``importlib.import_module("flashattention-gpt-oss-finetuning_amd")`` from the repository root.
 """
-from .attention import (FlashSWDAWithLearnedSinks, FlashSWDAWithSink, flash_swda_with_sink,  # noqa: F401
-                        swa_sink_attention)
+from .attention import (FlashSWDAWithLearnedSinks, FlashSWDAWithSink, FlashSWDAWithSinkVarlen,  # noqa: F401
+                        flash_swda_with_sink, flash_swda_with_sink_varlen, swa_sink_attention)
 from .gpt_oss import attention, gpt_oss_attention_forward, register_transformers  # noqa: F401
 from .flops import Workload, allowed_pairs_per_head  # noqa: F401
 
@@ -24,6 +28,8 @@ __all__ = [
     "flash_swda_with_sink",
     "swa_sink_attention",
     "FlashSWDAWithLearnedSinks",
+    "FlashSWDAWithSinkVarlen",
+    "flash_swda_with_sink_varlen",
     "attention",
     "gpt_oss_attention_forward",
     "register_transformers",

@@ -38,6 +38,8 @@ EXPORTS = (
     "fa_bwd_dkdv",
     "fa_fwd_sinks",
     "fa_bwd_sinks",
+    "fa_fwd_varlen",
+    "fa_bwd_varlen",
     "fa_bwd_workspace_bytes",
     "fa_check_fwd",
     "fa_check_bwd",
@@ -131,6 +133,12 @@ def lib() -> ctypes.CDLL:
             L.fa_bwd_sinks.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                        ctypes.c_size_t, ctypes.c_void_p]
             L.fa_bwd_sinks.restype = ctypes.c_int
+            L.fa_fwd_varlen.argtypes = [ctypes.POINTER(FwdParams), ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p,
+                                        ctypes.c_void_p]
+            L.fa_fwd_varlen.restype = ctypes.c_int
+            L.fa_bwd_varlen.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+            L.fa_bwd_varlen.restype = ctypes.c_int
             L.fa_bwd_workspace_bytes.argtypes = [ctypes.c_int32] * 7
             L.fa_bwd_workspace_bytes.restype = ctypes.c_size_t
             L.fa_check_fwd.argtypes = [ctypes.POINTER(FwdParams)]

@@ -234,3 +234,125 @@ def backward(q, k, v, o, lse, do, window: int, sink: int, scale: float, sinks=No
     if sinks is None:
         return call.dq, call.dk, call.dv
     return call.dq, call.dk, call.dv, call.dsinks
+
+
+# ---- variable-length batches ------------------------------------------------------------------
+
+def _check_packed(tensors, names):
+    """[total, H, D] packed tensors on one GPU with one supported dtype, all with the same number
+    of rows and head dim (the kernels bound every row they touch by q's row count)."""
+    for t, n in zip(tensors, names):
+        if t.dim() != 3:
+            raise ValueError(f"{n} must be 3-D [total, H, D], got shape {tuple(t.shape)}")
+    _check([t.unsqueeze(0) for t in tensors], names)
+    total, _, D = tensors[0].shape
+    for t, n in zip(tensors, names):
+        if t.shape[0] != total or t.shape[2] != D:
+            raise ValueError(f"{n} has shape {tuple(t.shape)}; packed tensors need {total} rows and head dim {D}")
+
+
+def _as_bhld(t: torch.Tensor) -> torch.Tensor:
+    """A packed [total, H, D] tensor as the [1, H, total, D] view the C ABI describes (the batch
+    stride is not used by the varlen entry points)."""
+    return _kernel_ready(t.permute(1, 0, 2).unsqueeze(0))
+
+
+def cu_seqlens_ready(cu_seqlens: torch.Tensor, total: int, device: torch.device, max_seqlen=None):
+    """cu_seqlens as the C ABI takes it -- int32 [B + 1] on the device -- and max_seqlen.
+
+    Offsets given on the host are checked (start at 0, non-decreasing, end within the packed
+    rows) and max_seqlen is computed when not given; offsets already on the device are used as
+    they are (checking them would synchronise the host), with max_seqlen required.  The kernels
+    clamp lengths and offsets either way, so bad device offsets give meaningless results, never
+    out-of-range memory accesses."""
+    if cu_seqlens.dim() != 1 or cu_seqlens.shape[0] < 2:
+        raise ValueError(f"cu_seqlens must be 1-D [B + 1] with B >= 1, got shape {tuple(cu_seqlens.shape)}")
+    if cu_seqlens.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"cu_seqlens must be an integer tensor, got {cu_seqlens.dtype}")
+    if cu_seqlens.device.type == "cpu":
+        c = cu_seqlens.to(torch.int64)
+        lens = c[1:] - c[:-1]
+        if int(c[0]) != 0 or bool((lens < 0).any()) or int(c[-1]) > total:
+            raise ValueError("cu_seqlens must start at 0, be non-decreasing and end at most at the number of "
+                             f"packed rows ({total}); got {c.tolist()}")
+        if max_seqlen is None:
+            max_seqlen = int(lens.max())
+        elif int(lens.max()) > int(max_seqlen):
+            raise ValueError(f"max_seqlen {max_seqlen} is below the longest sequence ({int(lens.max())})")
+    elif cu_seqlens.device != device:
+        raise RuntimeError(f"cu_seqlens is on {cu_seqlens.device} but q is on {device}")
+    elif max_seqlen is None:
+        raise ValueError("max_seqlen is required when cu_seqlens is on the GPU")
+    return cu_seqlens.to(device=device, dtype=torch.int32).contiguous(), max(1, int(max_seqlen))
+
+
+def forward_varlen(q, k, v, cu_seqlens, max_seqlen: int, window: int, sink: int, scale: float, sinks=None):
+    """Returns (o [total, Hq, D], lse float32 [Hq, total]) for packed q [total, Hq, D] and
+    k/v [total, Hkv, D]; cu_seqlens int32 [B + 1] on the device (see cu_seqlens_ready)."""
+    _check_packed((q, k, v), ("q", "k", "v"))
+    total, Hq, D = q.shape
+    Hkv = k.shape[1]
+    B = cu_seqlens.shape[0] - 1
+    qv, kv, vv = _as_bhld(q), _as_bhld(k), _as_bhld(v)
+    o = torch.empty((total, Hq, D), dtype=q.dtype, device=q.device)
+    lse = torch.empty((Hq, total), dtype=torch.float32, device=q.device)
+    ov = o.permute(1, 0, 2).unsqueeze(0)
+    sk = None if sinks is None else _sinks_ready(sinks, Hq, q.device)
+    p = _lib.FwdParams()
+    p.q, p.k, p.v = qv.data_ptr(), kv.data_ptr(), vv.data_ptr()
+    p.o, p.lse = ov.data_ptr(), lse.data_ptr()
+    p.q_stride[:] = _strides3(qv)
+    p.k_stride[:] = _strides3(kv)
+    p.v_stride[:] = _strides3(vv)
+    p.o_stride[:] = _strides3(ov)
+    p.lse_stride[:] = (0, lse.stride(0), lse.stride(1))
+    p.batch, p.heads_q, p.heads_kv, p.seqlen, p.head_dim = B, Hq, Hkv, _i32(max_seqlen), D
+    p.window, p.sink = _i32(window), _i32(sink)
+    p.softmax_scale = scale
+    p.dtype = _DTYPES[q.dtype]
+    with _DeviceGuard(q.device):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(q.device).cuda_stream)
+        rc = _lib.lib().fa_fwd_varlen(ctypes.byref(p), ctypes.c_void_p(cu_seqlens.data_ptr()), _i32(total),
+                                      ctypes.c_void_p(None if sk is None else sk.data_ptr()), stream)
+    _lib.raise_for_status(rc, "fa_fwd_varlen")
+    return o, lse
+
+
+def backward_varlen(q, k, v, o, lse, do, cu_seqlens, max_seqlen: int, window: int, sink: int, scale: float,
+                    sinks=None):
+    """Returns (dq, dk, dv) packed like q, k, v (and dsinks float32 [Hq] with learned sinks)."""
+    _check_packed((q, k, v, o, do), ("q", "k", "v", "o", "do"))
+    total, Hq, D = q.shape
+    Hkv = k.shape[1]
+    B = cu_seqlens.shape[0] - 1
+    qv, kv, vv, ovw, dov = (_as_bhld(t) for t in (q, k, v, o, do))
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    dqv, dkv, dvv = (t.permute(1, 0, 2).unsqueeze(0) for t in (dq, dk, dv))
+    sk = None if sinks is None else _sinks_ready(sinks, Hq, q.device)
+    dsinks = None if sinks is None else torch.empty(Hq, dtype=torch.float32, device=q.device)
+    ws_bytes = workspace_bytes(B, Hq, Hkv, int(max_seqlen), D, window, sink)
+    ws = torch.empty((max(ws_bytes, 256),), dtype=torch.uint8, device=q.device)
+    p = _lib.BwdParams()
+    p.q, p.k, p.v, p.o, p.dout = qv.data_ptr(), kv.data_ptr(), vv.data_ptr(), ovw.data_ptr(), dov.data_ptr()
+    p.lse = lse.data_ptr()
+    p.dq, p.dk, p.dv = dqv.data_ptr(), dkv.data_ptr(), dvv.data_ptr()
+    for field, t in (("q_stride", qv), ("k_stride", kv), ("v_stride", vv), ("o_stride", ovw), ("do_stride", dov),
+                     ("dq_stride", dqv), ("dk_stride", dkv), ("dv_stride", dvv)):
+        getattr(p, field)[:] = _strides3(t)
+    p.lse_stride[:] = (0, lse.stride(0), lse.stride(1))
+    p.batch, p.heads_q, p.heads_kv, p.seqlen, p.head_dim = B, Hq, Hkv, _i32(max_seqlen), D
+    p.window, p.sink = _i32(window), _i32(sink)
+    p.softmax_scale = scale
+    p.dtype = _DTYPES[q.dtype]
+    with _DeviceGuard(q.device):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(q.device).cuda_stream)
+        rc = _lib.lib().fa_bwd_varlen(ctypes.byref(p), ctypes.c_void_p(cu_seqlens.data_ptr()), _i32(total),
+                                      ctypes.c_void_p(None if sk is None else sk.data_ptr()),
+                                      ctypes.c_void_p(None if dsinks is None else dsinks.data_ptr()),
+                                      ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(ws.numel()), stream)
+    _lib.raise_for_status(rc, "fa_bwd_varlen")
+    if sinks is None:
+        return dq, dk, dv
+    return dq, dk, dv, dsinks

@@ -85,6 +85,53 @@ class FlashSWDAWithLearnedSinks(torch.autograd.Function):
         return dq, dk, dv, dsinks.to(sinks.dtype), None, None, None
 
 
+class FlashSWDAWithSinkVarlen(torch.autograd.Function):
+    """Variable-length (packed) batches of the same attention.
+
+    forward(q [total, Hq, D], k [total, Hkv, D], v [total, Hkv, D], cu_seqlens [B + 1],
+            max_seqlen, window_size, sink_size, softmax_scale=None, sinks=None) -> o [total, Hq, D]
+    Sequence b is rows [cu_seqlens[b], cu_seqlens[b + 1]) of every tensor; causality, the window
+    and the sink_size positional sinks apply within each sequence.  `sinks` optionally adds
+    GPT-OSS learned sink logits ([Hq]).  The reference takes fixed [B, H, L, D] batches only
+    (flash_attention_gpt_oss.py:348); this is the layout of packed finetuning batches.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, cu_seqlens, max_seqlen, window_size, sink_size, softmax_scale=None, sinks=None):
+        if softmax_scale is None:
+            softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+        if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+            raise AssertionError("Packed inputs must be 3-D [total, H, D]")
+        _check_shapes(q.unsqueeze(0).transpose(1, 2), k.unsqueeze(0).transpose(1, 2), v.unsqueeze(0).transpose(1, 2))
+        cu, max_seqlen = _ops.cu_seqlens_ready(cu_seqlens, q.shape[0], q.device, max_seqlen)
+        if window_size is None:
+            window_size = max_seqlen
+        o, lse = _ops.forward_varlen(q, k, v, cu, max_seqlen, int(window_size), int(sink_size), float(softmax_scale),
+                                     sinks=sinks)
+        ctx.save_for_backward(q, k, v, o, lse, cu, sinks)
+        ctx.softmax_scale = softmax_scale
+        ctx.window_size = window_size
+        ctx.sink_size = sink_size
+        ctx.max_seqlen = max_seqlen
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse, cu, sinks = ctx.saved_tensors
+        out = _ops.backward_varlen(q, k, v, o, lse, do, cu, ctx.max_seqlen, int(ctx.window_size), int(ctx.sink_size),
+                                   float(ctx.softmax_scale), sinks=sinks)
+        dsinks = None if sinks is None else out[3].to(sinks.dtype)
+        return out[0], out[1], out[2], None, None, None, None, None, dsinks
+
+
+def flash_swda_with_sink_varlen(q, k, v, cu_seqlens, max_seqlen, window_size, sink_size: int = 0,
+                                scale: Optional[float] = None, sinks=None):
+    """Functional form of FlashSWDAWithSinkVarlen: packed q [total, Hq, D], k/v [total, Hkv, D],
+    cu_seqlens [B + 1] (int32 or int64; on the host it is validated, on the GPU max_seqlen is
+    required), window_size None for full causal attention."""
+    return FlashSWDAWithSinkVarlen.apply(q, k, v, cu_seqlens, max_seqlen, window_size, sink_size, scale, sinks)
+
+
 def _check_shapes(q, k, v):
     """The shape conditions of flash_attention_gpt_oss.py:347-354, same messages."""
     if not (q.shape[0] == v.shape[0] and q.shape[2] == v.shape[2] and q.shape[3] == v.shape[3]):

@@ -46,12 +46,38 @@ struct Args {
   int chunk_rows;
   int n_chunk_wgs;   // B * Hkv * nsp * n_chunks
   int srows;         // sink rows stored per block in the partial sums: min(S, 64)
-  // sink rows in the dQ kernel (dq_sink_mode): rows >= sink_row0 add the sink keys' dK/dV there
+  // sink rows in the dQ kernel (dq_sink_mode): rows past key block 0's window add the sink keys'
+  // dK/dV there
   int sink_dq;       // 1 in that mode
-  int sink_row0;
   float* dq_sink_part;  // [n_tiles][dK, dV][srows][D] fp32: a run's sums at the slot of its first tile
   int dq_wgs;           // the dQ kernel's grid (set for the sink fold)
+  // variable-length batches: NULL, or [B + 1] device offsets of the sequences' first rows in
+  // tensors of total_rows packed rows (L is then the longest sequence, batch strides are 0)
+  const int* cu_seqlens;
+  int total_rows;
 };
+
+// Sequence b: its length and the row where it starts in the packed tensors (fixed-length
+// batches: L rows from row 0 of batch b's slice).  Offsets are clamped to the tensors' rows and
+// lengths to L, so malformed offsets cannot address memory outside the tensors.
+struct Seq {
+  int L;
+  int64_t row;
+};
+
+__device__ __forceinline__ Seq seq_of(const Args& a, int b) {
+  if (!a.cu_seqlens) return Seq{a.L, 0};
+  int lo = a.cu_seqlens[b], hi = a.cu_seqlens[b + 1];
+  lo = lo < 0 ? 0 : (lo > a.total_rows ? a.total_rows : lo);
+  hi = hi < lo ? lo : (hi > a.total_rows ? a.total_rows : hi);
+  const int n = hi - lo;
+  return Seq{n < a.L ? n : a.L, lo};
+}
+
+// Element offset of row `row` of (batch b, head h) of a tensor with strides s[3].
+__device__ __forceinline__ int64_t slice_off(const int64_t s[3], int b, int h, int64_t row) {
+  return int64_t(b) * s[0] + int64_t(h) * s[1] + row * s[2];
+}
 
 // Launchers (return the hipError_t of the launch; launch_bwd_dkdv also launches the sink fold).
 hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stream);

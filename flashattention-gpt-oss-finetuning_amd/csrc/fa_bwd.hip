@@ -72,7 +72,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   // scalar (no per-lane copies, no waterfall loops around buffer loads)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hf = lane >> 5;
-  const int L = a.L, W = a.W, S = a.S;
+  const int W = a.W, S = a.S;
 
   // this workgroup's tiles: its XCD's range [t_lo, t_hi), from pos with stride wgs_x
   const int groups = a.B * a.Hq / a.wh;
@@ -83,15 +83,19 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   // tiles per (batch, KV head): n_qtiles row tiles of each of the G / wh head groups
   const int tiles_per_kv = a.n_qtiles * (a.G / a.wh);
 
-  // tile -> (b, KV head, this wave's head hw, first row qw)
+  // tile -> (b, KV head, this wave's head hw, first row qw, the sequence's length L and first row)
   struct TileIdx {
-    int b, kvh, hw, q0, qw;
+    int b, kvh, hw, q0, qw, L;
+    int64_t row;
   };
   auto decode = [&](int tile) {
     TileIdx t;
     const int qt = tile % a.n_qtiles, hg = tile / a.n_qtiles;
     const int groups_per_batch = a.Hq / a.wh;
     t.b = hg / groups_per_batch;
+    const Seq sq = seq_of(a, t.b);
+    t.L = sq.L;
+    t.row = sq.row;
     const int h0 = (hg % groups_per_batch) * a.wh;
     t.kvh = h0 / a.G;
     t.q0 = qt * 32 * a.wq;
@@ -104,15 +108,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   // swizzled row-major [32][D] tiles (DMA instruction p, lane l fills 16-byte position 64p + l, so
   // it loads the global chunk that the swizzle places there), where they occupy no registers
   // while the current tile computes; the row's lse goes to a register.  Buffer resources over the
-  // head's rows [0, L): rows past L read as zero.
+  // sequence's rows [0, L) of the head: rows past L read as zero.
   uint16_t* stash = lds + 2 * BUF + wave * STASH;
-  const uint32_t nq = span_bytes(L, a.sq[2], D), nd = span_bytes(L, a.sdo[2], D), no = span_bytes(L, a.so[2], D);
-  const uint32_t nl = uint32_t((int64_t(L - 1) * a.slse[2] + 1) * 4);
   constexpr int CPR = D / 8;  // 16-byte chunks per row
   auto stash_rows = [&](const TileIdx& t) {
-    const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(a.q) + 2 * (int64_t(t.b) * a.sq[0] + int64_t(t.hw) * a.sq[1]), nq);
-    const rsrc_t rd = make_rsrc(reinterpret_cast<const char*>(a.dout) + 2 * (int64_t(t.b) * a.sdo[0] + int64_t(t.hw) * a.sdo[1]), nd);
-    const rsrc_t ro = make_rsrc(reinterpret_cast<const char*>(a.o) + 2 * (int64_t(t.b) * a.so[0] + int64_t(t.hw) * a.so[1]), no);
+    const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(a.q) + 2 * slice_off(a.sq, t.b, t.hw, t.row), span_bytes(t.L, a.sq[2], D));
+    const rsrc_t rd = make_rsrc(reinterpret_cast<const char*>(a.dout) + 2 * slice_off(a.sdo, t.b, t.hw, t.row), span_bytes(t.L, a.sdo[2], D));
+    const rsrc_t ro = make_rsrc(reinterpret_cast<const char*>(a.o) + 2 * slice_off(a.so, t.b, t.hw, t.row), span_bytes(t.L, a.so[2], D));
 #pragma unroll
     for (int p = 0; p < KS; ++p) {
       const int tr = (64 * p + lane) / CPR;  // tile row of this lane's 16-byte position
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
     }
   };
   auto load_lse = [&](const TileIdx& t) {
-    const rsrc_t rl = make_rsrc(a.lse + int64_t(t.b) * a.slse[0] + int64_t(t.hw) * a.slse[1], nl);
+    const rsrc_t rl = make_rsrc(a.lse + slice_off(a.slse, t.b, t.hw, t.row), span_f32(t.L, a.slse[2]));
     return buf_ldf(rl, uint32_t(int64_t(t.qw + r32) * a.slse[2] * 4));
   };
 
@@ -140,7 +142,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
     off_l[it] = swz_off<D>(row, 8 * col);
   }
   const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
-  const uint32_t nk_bytes = span_bytes(L, a.sk[2], D), nv_bytes = span_bytes(L, a.sv[2], D);
 
   // sink accumulators: lane l holds key 4(l/16) + i, head-dim column 16 nb + l % 16
   f32x4 dks[SINK ? NB16 : 1], dvs[SINK ? NB16 : 1];
@@ -164,7 +165,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   }
   for (; tile < t_hi; tile += wgs_x) {
     const TileIdx t = decode(tile);
-    const int qw = t.qw, q = qw + r32;
+    const int qw = t.qw, q = qw + r32, L = t.L;
     const bool wave_active = qw < L;
     const bool has_next = tile + wgs_x < t_hi;
 
@@ -195,16 +196,17 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
       for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m);
       if (lane == 0) a.dsink_part[(int64_t(t.b) * a.Hq + t.hw) * (a.Lp / 32) + qw / 32] = -v;
     }
-    // this wave's rows add to the sink keys' gradients (rows from sink_row0 on)
-    const bool sink_rows = SINK && wave_active && qw + 31 >= a.sink_row0;
+    // this wave's rows add to the sink keys' gradients (rows past key block 0's window)
+    const int sink_row0 = dq_sink_row0(L, W);
+    const bool sink_rows = SINK && wave_active && qw + 31 >= sink_row0;
 
     f32x16 acc[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
 
     const QPlan plan = qplan(t.q0, 32 * a.wq, L, W, S);
-    const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * (int64_t(t.b) * a.sk[0] + int64_t(t.kvh) * a.sk[1]), nk_bytes);
-    const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * (int64_t(t.b) * a.sv[0] + int64_t(t.kvh) * a.sv[1]), nv_bytes);
+    const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * slice_off(a.sk, t.b, t.kvh, t.row), span_bytes(L, a.sk[2], D));
+    const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * slice_off(a.sv, t.b, t.kvh, t.row), span_bytes(L, a.sv[2], D));
     u32x4 kreg[NK], vreg[NK];
     auto gload = [&](int kb) {
 #pragma unroll
@@ -312,7 +314,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
             if (ks0 == 0 && sink_rows) {
               // P and dS of keys [0, 16) (registers 0..7: keys 4hf + 0..3 and 8 + 4hf + 0..3 of
               // row q), rows before sink_row0 zeroed, into the [32 rows][16 keys] tiles
-              const bool row_on = q >= a.sink_row0;
+              const bool row_on = q >= sink_row0;
               float pz[8], dz[8];
 #pragma unroll
               for (int e = 0; e < 8; ++e) {
@@ -358,8 +360,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     if (wave_active && q < L) {
-      char* dqp = reinterpret_cast<char*>(a.dq) +
-                  2 * (int64_t(t.b) * a.sdq[0] + int64_t(t.hw) * a.sdq[1] + int64_t(q) * a.sdq[2]);
+      char* dqp = reinterpret_cast<char*>(a.dq) + 2 * slice_off(a.sdq, t.b, t.hw, t.row + q);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         if (D == 16 && hf == 1) continue;
@@ -448,7 +449,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hf = lane >> 5;
   const int kh = wave & 1, hh = wave >> 1;
-  const int L = a.L, W = a.W, S = a.S, G = a.G;
+  const int W = a.W, S = a.S, G = a.G;
 
   // Workgroups come in groups per (b, KV head): the n_kblocks regular ones, then the sink
   // chunks.  A group's workgroups land on one XCD (they share its L2), and the short chunk
@@ -457,6 +458,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int grp = id / per_group, r = id % per_group;
   const int kvh = grp % a.Hkv, b = grp / a.Hkv;
+  const Seq sq = seq_of(a, b);
+  const int L = sq.L;
   int kblk, chunk = -1, qlo, qhi;
   if (r < a.n_kblocks) {
     kblk = r;
@@ -469,6 +472,9 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
     qlo = kv_chunk_lo(kblk, chunk, a.chunk_rows, L, W);
     qhi = kv_chunk_hi(kblk, chunk, a.chunk_rows, L, W);
   }
+  // a key block past the end of its sequence (variable-length batches) has nothing to do; the
+  // sink fold reads no slot of it
+  if (kKvKeys * kblk >= L) return;
   const bool is_chunk = chunk >= 0;
   const bool partial_block = kblk < a.nsp;
   const int ks0 = kKvKeys * kblk + 32 * kh;  // this wave's keys
@@ -481,10 +487,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   // need no per-item sign handling.
   u32x4 kf[KS], vf[KS];
   {
-    const char* kp = reinterpret_cast<const char*>(a.k) +
-                     2 * (int64_t(b) * a.sk[0] + int64_t(kvh) * a.sk[1] + int64_t(key) * a.sk[2]);
-    const char* vp = reinterpret_cast<const char*>(a.v) +
-                     2 * (int64_t(b) * a.sv[0] + int64_t(kvh) * a.sv[1] + int64_t(key) * a.sv[2]);
+    const char* kp = reinterpret_cast<const char*>(a.k) + 2 * slice_off(a.sk, b, kvh, sq.row + key);
+    const char* vp = reinterpret_cast<const char*>(a.v) + 2 * slice_off(a.sv, b, kvh, sq.row + key);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int d = hf * (D / 2) + 8 * ks;
@@ -528,14 +532,14 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
     const int col = phys ^ swz<D>(row);        // the logical chunk stored there
     dma_off[p] = uint32_t((int64_t(row) * t_rs + 8 * col) * 2);
   }
-  const char* qslice = reinterpret_cast<const char*>(a.q) + 2 * (int64_t(b) * a.sq[0] + int64_t(kvh) * G * a.sq[1]);
-  const char* dslice = reinterpret_cast<const char*>(a.dout) + 2 * (int64_t(b) * a.sdo[0] + int64_t(kvh) * G * a.sdo[1]);
-  const char* lslice = reinterpret_cast<const char*>(a.lse + int64_t(b) * a.slse[0] + int64_t(kvh) * G * a.slse[1]);
+  const char* qslice = reinterpret_cast<const char*>(a.q) + 2 * slice_off(a.sq, b, kvh * G, sq.row);
+  const char* dslice = reinterpret_cast<const char*>(a.dout) + 2 * slice_off(a.sdo, b, kvh * G, sq.row);
+  const char* lslice = reinterpret_cast<const char*>(a.lse + slice_off(a.slse, b, kvh * G, sq.row));
   const char* tslice = reinterpret_cast<const char*>(a.delta + (int64_t(b) * a.Hq + int64_t(kvh) * G) * a.Lp);
   const char* tile_slice = t_kind ? dslice : qslice;
   const int64_t t_hs = t_kind ? a.sdo[1] : a.sq[1];  // head stride of the tile's tensor
   const uint32_t nt_bytes = span_bytes(L, t_rs, D);
-  const uint32_t nl = uint32_t((int64_t(L - 1) * a.slse[2] + 1) * 4), nt = uint32_t(L * 4);
+  const uint32_t nl = span_f32(L, a.slse[2]), nt = uint32_t(L * 4);
   // bytes per 32-row block
   const uint32_t bt = uint32_t(64 * t_rs), bl = uint32_t(128 * a.slse[2]);
   // stats: thread tid < 128 loads row tid % 32 of (slot tid / 64, kind (tid / 32) % 2).  Every
@@ -750,10 +754,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
               f32x4{dv[db][4 * e4], dv[db][4 * e4 + 1], dv[db][4 * e4 + 2], dv[db][4 * e4 + 3]};
         }
       } else if (!is_chunk) {
-        char* dkp = reinterpret_cast<char*>(a.dk) +
-                    2 * (int64_t(b) * a.sdk[0] + int64_t(kvh) * a.sdk[1] + int64_t(key) * a.sdk[2]);
-        char* dvp = reinterpret_cast<char*>(a.dv) +
-                    2 * (int64_t(b) * a.sdv[0] + int64_t(kvh) * a.sdv[1] + int64_t(key) * a.sdv[2]);
+        char* dkp = reinterpret_cast<char*>(a.dk) + 2 * slice_off(a.sdk, b, kvh, sq.row + key);
+        char* dvp = reinterpret_cast<char*>(a.dv) + 2 * slice_off(a.sdv, b, kvh, sq.row + key);
         float kv[16], vv[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
@@ -787,6 +789,8 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
   const int key = blockIdx.x % nrows;
   const int bh = blockIdx.x / nrows;  // b * Hkv + kvh
   const int kvh = bh % a.Hkv, b = bh / a.Hkv;
+  const Seq sq = seq_of(a, b);
+  if (key >= sq.L) return;  // a sink key past the end of a short sequence: no such row
   const int kblk = key / kKvKeys, row = key % kKvKeys;
   const int d = threadIdx.x % D, g = threadIdx.x / D;
   const int64_t blk = int64_t(bh) * a.nsp + kblk;
@@ -854,10 +858,8 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
     tv += part[1][j][d];
   }
   const uint32_t pk = E::pack2(tk * a.scale, tv);
-  reinterpret_cast<uint16_t*>(a.dk)[int64_t(b) * a.sdk[0] + int64_t(kvh) * a.sdk[1] + int64_t(key) * a.sdk[2] + d] =
-      uint16_t(pk);
-  reinterpret_cast<uint16_t*>(a.dv)[int64_t(b) * a.sdv[0] + int64_t(kvh) * a.sdv[1] + int64_t(key) * a.sdv[2] + d] =
-      uint16_t(pk >> 16);
+  reinterpret_cast<uint16_t*>(a.dk)[slice_off(a.sdk, b, kvh, sq.row + key) + d] = uint16_t(pk);
+  reinterpret_cast<uint16_t*>(a.dv)[slice_off(a.sdv, b, kvh, sq.row + key) + d] = uint16_t(pk >> 16);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -873,7 +875,8 @@ __global__ __launch_bounds__(256) void bwd_sink_logit_kernel(const Args a) {
   float acc = 0.f;
   for (int64_t i = tid; i < n; i += 256) {
     const int64_t b = i / nb, j = i % nb;
-    acc += a.dsink_part[(b * a.Hq + h) * nb + j];
+    // row blocks past the end of a short sequence hold no partial
+    if (32 * j < seq_of(a, int(b)).L) acc += a.dsink_part[(b * a.Hq + h) * nb + j];
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);

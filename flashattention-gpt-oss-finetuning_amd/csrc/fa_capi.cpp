@@ -189,7 +189,22 @@ int fa_check_bwd(const fa_bwd_params* p) {
 
 namespace {
 
-int run_fwd(const fa_fwd_params* p, const float* sinks, void* stream) {
+// Variable-length batches: the sequences' rows are packed, so the batch strides are unused.
+int check_varlen(const int32_t* cu_seqlens, int32_t total_rows) {
+  if (!cu_seqlens) return FA_ERR_NULL;
+  if (!aligned4(cu_seqlens)) return FA_ERR_ALIGN;
+  if (total_rows < 0) return FA_ERR_SHAPE;
+  return FA_OK;
+}
+
+void set_varlen(fa::Args* a, const int32_t* cu_seqlens, int32_t total_rows) {
+  a->cu_seqlens = cu_seqlens;
+  a->total_rows = total_rows;
+  for (int64_t* st : {a->sq, a->sk, a->sv, a->so, a->sdo, a->slse, a->sdq, a->sdk, a->sdv, a->so_out}) st[0] = 0;
+}
+
+int run_fwd(const fa_fwd_params* p, const float* sinks, void* stream, const int32_t* cu_seqlens = nullptr,
+            int32_t total_rows = 0) {
   fa::Args a = base_args(p->batch, p->heads_q, p->heads_kv, p->seqlen, p->head_dim, p->window, p->sink,
                          p->softmax_scale);
   a.q = p->q;
@@ -203,6 +218,7 @@ int run_fwd(const fa_fwd_params* p, const float* sinks, void* stream) {
   copy3(a.sv, p->v_stride);
   copy3(a.so_out, p->o_stride);
   copy3(a.slse, p->lse_stride);
+  if (cu_seqlens) set_varlen(&a, cu_seqlens, total_rows);
   int hpw, wh, wq;
   choose_qmajor(a.G, p->head_dim <= 64 ? 2 : 1, &hpw, &wh, &wq);
   a.wh = wh;
@@ -219,6 +235,15 @@ extern "C" {
 int fa_fwd(const fa_fwd_params* p, void* stream) {
   const int rc = fa_check_fwd(p);
   return rc != FA_OK ? rc : run_fwd(p, nullptr, stream);
+}
+
+int fa_fwd_varlen(const fa_fwd_params* p, const int32_t* cu_seqlens, int32_t total_rows, const float* sinks,
+                  void* stream) {
+  int rc = fa_check_fwd(p);
+  if (rc == FA_OK) rc = check_varlen(cu_seqlens, total_rows);
+  if (rc != FA_OK) return rc;
+  if (sinks && !aligned4(sinks)) return FA_ERR_ALIGN;
+  return run_fwd(p, sinks, stream, cu_seqlens, total_rows);
 }
 
 int fa_fwd_sinks(const fa_fwd_params* p, const float* sinks, void* stream) {
@@ -285,7 +310,6 @@ int prepare_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
   a.dsink_part = reinterpret_cast<float*>(ws + off_dsink);
   const size_t off_dq_slots = off_dsink + dsink_part_bytes(a.B, a.Hq, a.L);
   a.sink_dq = sp.dq;
-  a.sink_row0 = fa::dq_sink_row0(a.L, a.W);
   if (sp.dq) a.dq_sink_part = reinterpret_cast<float*>(ws + off_dq_slots);
   a.n_kblocks = (a.L + fa::kKvKeys - 1) / fa::kKvKeys;
   a.nsp = sp.nsp;
@@ -332,6 +356,24 @@ int fa_bwd_sinks(const fa_bwd_params* p, const float* sinks, float* dsinks, void
   const hipStream_t s = static_cast<hipStream_t>(stream);
   int r = run_dq(a, p, hpw, s);
   if (r == FA_OK) r = fa::launch_bwd_sink_logits(a, s) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+  return r != FA_OK ? r : run_dkdv(a, p, s);
+}
+
+int fa_bwd_varlen(const fa_bwd_params* p, const int32_t* cu_seqlens, int32_t total_rows, const float* sinks,
+                  float* dsinks, void* workspace, size_t workspace_bytes, void* stream) {
+  fa::Args a;
+  int hpw = 1;
+  int rc = prepare_bwd(p, workspace, workspace_bytes, &a, &hpw);
+  if (rc == FA_OK) rc = check_varlen(cu_seqlens, total_rows);
+  if (rc != FA_OK) return rc;
+  if (!sinks != !dsinks) return FA_ERR_NULL;
+  if ((sinks && !aligned4(sinks)) || (dsinks && !aligned4(dsinks))) return FA_ERR_ALIGN;
+  set_varlen(&a, cu_seqlens, total_rows);
+  a.sink_logits = sinks;
+  a.dsink = dsinks;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int r = run_dq(a, p, hpw, s);
+  if (r == FA_OK && sinks) r = fa::launch_bwd_sink_logits(a, s) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
   return r != FA_OK ? r : run_dkdv(a, p, s);
 }
 

@@ -148,6 +148,10 @@ __device__ __forceinline__ float buf_ldf(rsrc_t r, uint32_t off) {
 __device__ __forceinline__ void buf_dma16(rsrc_t r, uint16_t* lds_dst, uint32_t off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds_dst), 16, off, 0, 0, 0);
 }
+// Bytes spanned by `rows` fp32 values with stride `stride` (0 if none).
+__device__ __forceinline__ uint32_t span_f32(int rows, int64_t stride) {
+  return rows > 0 ? uint32_t((int64_t(rows - 1) * stride + 1) * 4) : 0u;
+}
 // Bytes spanned by `rows` rows of `cols` 16-bit elements with row stride `stride` (0 if none).
 __device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride, int cols) {
   return rows > 0 ? uint32_t((int64_t(rows - 1) * stride + cols) * 2) : 0u;

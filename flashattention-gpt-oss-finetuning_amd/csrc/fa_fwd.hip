@@ -188,7 +188,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // scalar (no per-lane copies, no waterfall loops around buffer loads)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, hf = lane >> 5;
-  const int L = a.L, W = a.W, S = a.S;
+  const int W = a.W, S = a.S;
 
   // this workgroup's tiles: its XCD's contiguous range [t_lo, t_hi), from pos with stride
   // wgs_x (neighbouring tiles share K/V rows in that XCD's L2)
@@ -199,14 +199,19 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   const int per = n_tiles / NX, rem = n_tiles % NX;
   const int t_lo = xcd * per + min(xcd, rem), t_hi = t_lo + per + (xcd < rem ? 1 : 0);
 
-  // tile -> (b, KV head, this wave's first head hw, first row of the tile q0 and of the wave qw)
+  // tile -> (b, KV head, this wave's first head hw, first row of the tile q0 and of the wave qw,
+  // the sequence's length L and first row)
   struct TileIdx {
-    int b, kvh, hw, q0, qw;
+    int b, kvh, hw, q0, qw, L;
+    int64_t row;
   };
   auto decode = [&](int tile) {
     TileIdx t;
     const int qt = tile % a.n_qtiles, hg = tile / a.n_qtiles;
     t.b = hg / groups_per_batch;
+    const Seq sq = seq_of(a, t.b);
+    t.L = sq.L;
+    t.row = sq.row;
     const int h0 = (hg % groups_per_batch) * hwg;
     t.kvh = h0 / a.G;
     t.q0 = qt * 32 * a.wq;
@@ -217,11 +222,12 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
 
   // A tile's Q rows for this wave go by LDS DMA into the wave's own stash -- fragment (h, ks)
   // of lane l at 16 bytes each, in lane order -- so they occupy no registers while the current
-  // tile computes.  Buffer resources over the head's rows [0, L): rows past L read as zero.
+  // tile computes.  Buffer resources over the sequence's rows [0, L) of the head: rows past L
+  // read as zero.
   uint16_t* stash = lds + 2 * BUF + wave * STASH;
-  const uint32_t nq = span_bytes(L, a.sq[2], D);
   auto q_rsrc = [&](const TileIdx& t, int h) {
-    return make_rsrc(reinterpret_cast<const char*>(a.q) + 2 * (int64_t(t.b) * a.sq[0] + int64_t(t.hw + h) * a.sq[1]), nq);
+    return make_rsrc(reinterpret_cast<const char*>(a.q) + 2 * slice_off(a.sq, t.b, t.hw + h, t.row),
+                     span_bytes(t.L, a.sq[2], D));
   };
   auto q_off = [&](const TileIdx& t, int ks) {
     return uint32_t((int64_t(t.qw + r32) * a.sq[2] + hf * (D / 2) + 8 * ks) * 2);
@@ -243,7 +249,6 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   const uint32_t off_v0 = uint32_t((int64_t(row0) * a.sv[2] + 8 * col0) * 2);
   const int off_l0 = swz_off<D>(row0, 8 * col0);
   const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
-  const uint32_t nk_bytes = span_bytes(L, a.sk[2], D), nv_bytes = span_bytes(L, a.sv[2], D);
 
   // the recurring masks (made visible by the barrier before the first key block)
   float* const pat = reinterpret_cast<float*>(lds + 2 * BUF + 4 * STASH);
@@ -257,7 +262,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   }
   for (; tile < t_hi; tile += wgs_x) {
   const TileIdx t = decode(tile);
-  const int b = t.b, kvh = t.kvh, hw = t.hw, q0 = t.q0, qw = t.qw;
+  const int b = t.b, kvh = t.kvh, hw = t.hw, q0 = t.q0, qw = t.qw, L = t.L;
   const int BM = 32 * a.wq;
   const int q = qw + r32;
   const bool wave_active = qw < L;
@@ -291,12 +296,12 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // Key block enumeration for the workgroup's rows [q0, q_end).
   const QPlan plan = qplan(q0, BM, L, W, S);
 
-  // K/V of the KV head through buffer resources spanning rows [0, L): rows past L read as zero,
-  // so the loads need no branches (a slice is < 2^31 bytes, checked by the C ABI).
-  const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * (int64_t(b) * a.sk[0] + int64_t(kvh) * a.sk[1]),
-                              nk_bytes);
-  const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * (int64_t(b) * a.sv[0] + int64_t(kvh) * a.sv[1]),
-                              nv_bytes);
+  // K/V of the KV head through buffer resources spanning the sequence's rows [0, L): rows past L
+  // read as zero, so the loads need no branches (a slice is < 2^31 bytes, checked by the C ABI).
+  const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * slice_off(a.sk, b, kvh, t.row),
+                              span_bytes(L, a.sk[2], D));
+  const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * slice_off(a.sv, b, kvh, t.row),
+                              span_bytes(L, a.sv[2], D));
 
   // Register staging of the next LDS block.
   u32x4 kreg[NK], vreg[NK];
@@ -371,8 +376,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
       mt = mn;
     }
     const float inv = lt > 0.f ? r / lt : 0.f;
-    char* op = reinterpret_cast<char*>(a.o_out) +
-               2 * (int64_t(b) * a.so_out[0] + int64_t(hw + h) * a.so_out[1] + int64_t(q) * a.so_out[2]);
+    char* op = reinterpret_cast<char*>(a.o_out) + 2 * slice_off(a.so_out, b, hw + h, t.row + q);
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       if (D == 16 && hf == 1) continue;
@@ -384,7 +388,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
       st16(op + 2 * (d0 + 8), pack8<E>(ov + 8));
     }
     if (hf == 0) {
-      a.lse_out[int64_t(b) * a.slse[0] + int64_t(hw + h) * a.slse[1] + int64_t(q) * a.slse[2]] =
+      a.lse_out[slice_off(a.slse, b, hw + h, t.row + q)] =
           (mt + fast_log2(lt)) * kLn2;
     }
   }

@@ -38,6 +38,12 @@ struct QPlan {
 
 FA_HD QPlan qplan(int q0, int bm, int L, int W, int S) {
   QPlan p;
+  if (q0 >= L) {  // a tile past the end of its sequence (variable-length batches): nothing to visit
+    p.ws = 0;
+    p.nsb = 0;
+    p.nb = 0;
+    return p;
+  }
   const int q_end = imin(q0 + bm, L);
   p.ws = (imax(0, q0 - W + 1) / kLdsKeys) * kLdsKeys;
   const int sink_end = imin(S, p.ws);

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define FA_GFX950_VERSION 10100 /* 1.1.0 */
+#define FA_GFX950_VERSION 10200 /* 1.2.0 */
 
 /* Element types of q/k/v/o/dout/dq/dk/dv.  All of them share one type per call. */
 enum fa_dtype { FA_DTYPE_BF16 = 1, FA_DTYPE_F16 = 2 };
@@ -152,6 +152,26 @@ int fa_bwd_dkdv(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
 int fa_fwd_sinks(const fa_fwd_params* p, const float* sinks, void* stream);
 int fa_bwd_sinks(const fa_bwd_params* p, const float* sinks, float* dsinks, void* workspace,
                  size_t workspace_bytes, void* stream);
+
+/* Variable-length batches: `batch` sequences of different lengths whose rows are packed back to
+ * back, as in a finetuning batch of concatenated samples.  The reference has fixed [B, H, L, D]
+ * inputs only (flash_attention_gpt_oss.py:348); these entry points are the varlen form of
+ * fa_fwd / fa_fwd_sinks and fa_bwd / fa_bwd_sinks.
+ *   - q, o, dout, dq: [total_rows, Hq, D]; k, v, dk, dv: [total_rows, Hkv, D]; lse: float32 with
+ *     one value per (head, row), e.g. [Hq, total_rows].  The head and row strides of each tensor
+ *     are given as usual; batch strides are ignored.
+ *   - cu_seqlens: int32 [batch + 1] in DEVICE memory, cu_seqlens[0] = 0, non-decreasing,
+ *     cu_seqlens[batch] <= total_rows: sequence b is rows [cu_seqlens[b], cu_seqlens[b + 1]).
+ *   - p->seqlen: the longest sequence (lengths are clamped to it, offsets to total_rows, so bad
+ *     offsets cannot address memory outside the tensors; the results are then meaningless).
+ *   - Causality, the window and the S positional sinks apply within each sequence: a row never
+ *     sees another sequence's keys, and the sinks are each sequence's first S keys.
+ *   - sinks (float32 [Hq]) may be NULL; fa_bwd_varlen takes sinks and dsinks together or
+ *     neither.  The workspace is fa_bwd_workspace_bytes(batch, Hq, Hkv, p->seqlen, D, W, S). */
+int fa_fwd_varlen(const fa_fwd_params* p, const int32_t* cu_seqlens, int32_t total_rows, const float* sinks,
+                  void* stream);
+int fa_bwd_varlen(const fa_bwd_params* p, const int32_t* cu_seqlens, int32_t total_rows, const float* sinks,
+                  float* dsinks, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Host-only argument checks used by fa_fwd / fa_bwd (no HIP call is made). */
 int fa_check_fwd(const fa_fwd_params* p);

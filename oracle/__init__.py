@@ -10,7 +10,9 @@ Contents
                textbook forward in the input dtype (the reference's baseline), and an explicit
                float32/float64 forward + backward returning O, LSE, dQ, dK, dV; the same with
                GPT-OSS learned per-head sink logits (also returning their gradient), and a
-               restatement of HF transformers' eager GPT-OSS attention.
+               restatement of HF transformers' eager GPT-OSS attention; variable-length
+               (packed) batches as independent sequences, and the packed batch's
+               block-diagonal mask.
   loops.py  -- pure-Python double loop over (q, k) for tiny shapes: a second, independent
                statement of the mask and of the forward.
 
@@ -22,6 +24,8 @@ against the committed fixtures in tests/golden/ (computed with SDPA in float64).
 sinks are pinned against SDPA with one extra zero key whose additive mask column holds the sink
 logit (an independent statement of "a logit in the denominator without a value"), against the
 installed transformers package's own eager_attention_forward, against the no-sink oracle for a
-sink of -inf, and by gradcheck for the sink gradient.  The
+sink of -inf, and by gradcheck for the sink gradient.  The variable-length oracle is pinned
+against one SDPA call over the whole packed batch with the block-diagonal mask (and autograd
+for the gradients), and against single-sequence batches of the fixed-length oracle.  The
 reference ships no golden vectors of its own (it has no test suite).
 """

@@ -177,3 +177,56 @@ class OracleAttentionSinks(torch.autograd.Function):
         _, _, dq, dk, dv, ds = attention_fwd_bwd_sinks(q, k, v, sinks, do, window_size, sink_size, scale,
                                                         compute_dtype=q.dtype)
         return dq, dk, dv, ds, None, None, None
+
+
+@torch.no_grad()
+def attention_fwd_bwd_varlen(q, k, v, do, cu_seqlens, window_size: int, sink_size: int, scale: Optional[float] = None,
+                             sinks=None, compute_dtype=torch.float32, row_chunk: Optional[int] = None):
+    """Variable-length batches: packed q/do [total, Hq, D], k/v [total, Hkv, D]; sequence b is
+    rows [cu_seqlens[b], cu_seqlens[b + 1]) and is an independent instance of
+    attention_fwd_bwd (or attention_fwd_bwd_sinks with `sinks`).  Returns (o [total, Hq, D],
+    lse [Hq, total], dq, dk, dv) and, with sinks, dsinks summed over the sequences."""
+    total, Hq, D = q.shape
+    Hkv = k.shape[1]
+    o = torch.zeros((total, Hq, D), dtype=compute_dtype, device=q.device)
+    lse = torch.full((Hq, total), float("-inf"), dtype=compute_dtype, device=q.device)
+    dq = torch.zeros((total, Hq, D), dtype=compute_dtype, device=q.device)
+    dk = torch.zeros((total, Hkv, D), dtype=compute_dtype, device=q.device)
+    dv = torch.zeros((total, Hkv, D), dtype=compute_dtype, device=q.device)
+    dsinks = None if sinks is None else torch.zeros(Hq, dtype=compute_dtype, device=q.device)
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    as4 = lambda t, lo, hi: t[lo:hi].permute(1, 0, 2).unsqueeze(0)  # [1, H, L_b, D]
+    for lo, hi in zip(cu[:-1], cu[1:]):
+        if hi <= lo:
+            continue
+        args = (as4(q, lo, hi), as4(k, lo, hi), as4(v, lo, hi))
+        if sinks is None:
+            r = attention_fwd_bwd(*args, as4(do, lo, hi), window_size, sink_size, scale, compute_dtype, row_chunk)
+        else:
+            r = attention_fwd_bwd_sinks(*args, sinks, as4(do, lo, hi), window_size, sink_size, scale, compute_dtype,
+                                        row_chunk)
+            dsinks += r[5]
+        o[lo:hi] = r[0][0].permute(1, 0, 2)
+        lse[:, lo:hi] = r[1][0]
+        dq[lo:hi] = r[2][0].permute(1, 0, 2)
+        dk[lo:hi] = r[3][0].permute(1, 0, 2)
+        dv[lo:hi] = r[4][0].permute(1, 0, 2)
+    if sinks is None:
+        return o, lse, dq, dk, dv
+    return o, lse, dq, dk, dv, dsinks
+
+
+def packed_allowed_mask(cu_seqlens, window_size: int, sink_size: int, device=None) -> torch.Tensor:
+    """[total, total] bool for a packed batch: row r may see column c when both lie in the same
+    sequence and, with positions counted from that sequence's first row, allowed_mask holds."""
+    cu = [int(x) for x in cu_seqlens.tolist()]
+    total = cu[-1]
+    seq = torch.empty(total, dtype=torch.long, device=device)
+    start = torch.empty(total, dtype=torch.long, device=device)
+    for b, (lo, hi) in enumerate(zip(cu[:-1], cu[1:])):
+        seq[lo:hi] = b
+        start[lo:hi] = lo
+    pos = torch.arange(total, device=device) - start
+    qq, kk = pos.view(-1, 1), pos.view(1, -1)
+    same = seq.view(-1, 1) == seq.view(1, -1)
+    return same & (kk <= qq) & (((qq - kk) < window_size) | (kk < sink_size))

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_strerror():
     L = _lib.lib()
-    assert L.fa_version() == 10100
+    assert L.fa_version() == 10200
     codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10]
     texts = [_lib.strerror(c) for c in codes]
     assert len(set(texts)) == len(codes)
@@ -228,3 +228,20 @@ def test_workspace_bytes():
     # invalid problems give 0
     assert ws(1, 8, 3, 128, 64, 16, 4) == 0
     assert ws(1, 8, 2, 128, 64, 0, 0) == 0
+
+
+def test_varlen_entry_points_reject_before_any_hip_call():
+    """fa_fwd_varlen / fa_bwd_varlen check their extra arguments on the host; no GPU needed."""
+    L = _lib.lib()
+    ws = (ctypes.c_void_p(256), ctypes.c_size_t(1 << 30))
+    cu = ctypes.c_void_p(1024)
+    assert L.fa_fwd_varlen(ctypes.byref(_fwd_params()), None, 100, None, None) == _lib.FA_ERR_NULL
+    assert L.fa_fwd_varlen(ctypes.byref(_fwd_params()), ctypes.c_void_p(1026), 100, None, None) == _lib.FA_ERR_ALIGN
+    assert L.fa_fwd_varlen(ctypes.byref(_fwd_params()), cu, -1, None, None) == _lib.FA_ERR_SHAPE
+    assert L.fa_fwd_varlen(ctypes.byref(_fwd_params()), cu, 100, ctypes.c_void_p(514), None) == _lib.FA_ERR_ALIGN
+    assert L.fa_fwd_varlen(ctypes.byref(_fwd_params(head_dim=48)), cu, 100, None, None) == _lib.FA_ERR_HEAD_DIM
+    assert L.fa_bwd_varlen(ctypes.byref(_bwd_params()), None, 100, None, None, *ws, None) == _lib.FA_ERR_NULL
+    assert L.fa_bwd_varlen(ctypes.byref(_bwd_params()), cu, 100, ctypes.c_void_p(256), None, *ws,
+                           None) == _lib.FA_ERR_NULL
+    assert L.fa_bwd_varlen(ctypes.byref(_bwd_params()), cu, 100, None, None, ctypes.c_void_p(256),
+                           ctypes.c_size_t(0), None) == _lib.FA_ERR_WORKSPACE

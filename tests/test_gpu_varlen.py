@@ -1,0 +1,138 @@
+"""GPU parity of variable-length (packed) batches: fa_fwd_varlen / fa_bwd_varlen against the
+float32 variable-length oracle on the same seeded inputs.
+
+Same bar as tests/test_gpu_parity.py: elementwise |ours - ref| <= a + 2e-2 |ref| with
+a = max(2e-2, 2 x the max error of the reference's naive path in the input dtype), the naive
+path being run per sequence on the CPU.  Cases mix long, short, length-1 and empty sequences,
+both sink paths (S <= 16 in the dQ kernel, S > 16 in chunk workgroups), learned sinks, full
+causal attention and D in {16, 32, 64, 128}.
+"""
+import math
+
+import pytest
+import torch
+
+from conftest import load_mod, load_pkg
+from oracle import naive
+from test_gpu_parity import assert_close
+
+pytestmark = pytest.mark.gpu
+
+BF, FP = torch.bfloat16, torch.float16
+
+
+def packed_inputs(total, Hq, Hkv, D, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    mk = lambda *s: torch.randn(*s, generator=g).to(dtype).cuda()
+    return mk(total, Hq, D), mk(total, Hkv, D), mk(total, Hkv, D), mk(total, Hq, D)
+
+
+def naive_packed(q, k, v, do, cu, W, S, scale):
+    """The reference's naive path in the input dtype, sequence by sequence on the CPU."""
+    outs = [torch.zeros_like(t, device="cpu") for t in (q, q, k, v)]
+    for lo, hi in zip(cu[:-1], cu[1:]):
+        if hi <= lo:
+            continue
+        as4 = lambda t: t[lo:hi].detach().cpu().permute(1, 0, 2).unsqueeze(0).contiguous()
+        qc, kc, vc = (as4(t).requires_grad_() for t in (q, k, v))
+        o = naive.naive_attention(qc, kc, vc, W, S, scale=scale)
+        o.backward(as4(do))
+        for dst, src in zip(outs, (o.detach(), qc.grad, kc.grad, vc.grad)):
+            dst[lo:hi] = src[0].permute(1, 0, 2)
+    return outs
+
+
+def run_varlen(cu, Hq, Hkv, D, W, S, dtype, seed=0, sinks=False, with_naive=True):
+    ops = load_mod("_ops")
+    print(f"case cu={cu} Hq={Hq} Hkv={Hkv} D={D} W={W} S={S} {dtype} sinks={sinks}", flush=True)
+    total = cu[-1]
+    q, k, v, do = packed_inputs(total, Hq, Hkv, D, dtype, seed)
+    sk = torch.randn(Hq, generator=torch.Generator().manual_seed(seed + 1)).cuda() if sinks else None
+    scale = 1.0 / math.sqrt(D)
+    cu_dev, max_len = ops.cu_seqlens_ready(torch.tensor(cu, dtype=torch.int32), total, q.device)
+    Wk = max_len if W is None else W
+    o, lse = ops.forward_varlen(q, k, v, cu_dev, max_len, Wk, S, scale, sinks=sk)
+    grads = ops.backward_varlen(q, k, v, o, lse, do, cu_dev, max_len, Wk, S, scale, sinks=sk)
+    torch.cuda.synchronize()
+    ref = naive.attention_fwd_bwd_varlen(q, k, v, do, torch.tensor(cu), Wk, S, scale, sinks=sk,
+                                         compute_dtype=torch.float32, row_chunk=1024)
+    nv = naive_packed(q, k, v, do, cu, Wk, S, scale) if (with_naive and not sinks) else (None,) * 4
+    assert_close("O", o, ref[0], nv[0])
+    assert_close("LSE", lse, ref[1])
+    assert_close("dQ", grads[0], ref[2], nv[1])
+    assert_close("dK", grads[1], ref[3], nv[2])
+    assert_close("dV", grads[2], ref[4], nv[3])
+    if sinks:
+        err = (grads[3] - ref[5]).abs()
+        p_sink_delta = ref[5].abs() + 1.0
+        assert bool((err <= 2e-2 * p_sink_delta).all()), ("dsinks", float(err.max()))
+    return o, lse, grads
+
+
+@pytest.mark.parametrize("cu,Hq,Hkv,D,W,S,dtype", [
+    pytest.param([0, 300, 301, 1000, 1000, 1777], 8, 1, 64, 128, 4, BF, id="dq-sinks-mixed-lengths"),
+    pytest.param([0, 700, 1500], 4, 2, 64, 64, 40, FP, id="sink-chunks"),
+    pytest.param([0, 130, 900], 8, 2, 128, 100, 0, BF, id="D128-G4"),
+    pytest.param([0, 33, 97, 600], 4, 4, 16, 40, 16, FP, id="D16-G1"),
+    pytest.param([0, 500, 1200], 4, 1, 32, None, 0, BF, id="full-causal-D32"),
+    pytest.param([0, 64, 128, 192, 256], 16, 2, 64, 32, 4, BF, id="equal-lengths"),
+    pytest.param([0, 0, 1, 1, 2], 2, 1, 64, 8, 1, FP, id="tiny-and-empty"),
+    pytest.param([0, 2048, 4096], 64, 8, 64, 128, 4, BF, id="gpt-oss-shape-two-sequences"),
+])
+def test_varlen_parity(gpu, cu, Hq, Hkv, D, W, S, dtype):
+    run_varlen(cu, Hq, Hkv, D, W, S, dtype, seed=cu[-1] % 97 + D, with_naive=cu[-1] * Hq <= 1 << 16)
+
+
+def test_varlen_learned_sinks(gpu):
+    run_varlen([0, 250, 700, 701], 8, 1, 64, 128, 0, BF, seed=11, sinks=True)
+
+
+def test_varlen_matches_separate_fixed_length_calls(gpu):
+    """Each packed sequence gets exactly what a fixed-length call on it alone gets: O, LSE and
+    dQ bitwise; dK/dV to rounding (their sink rows are summed in a different grouping)."""
+    ops = load_mod("_ops")
+    cu = [0, 200, 650, 651, 1100]
+    Hq, Hkv, D, W, S = 8, 1, 64, 64, 4
+    q, k, v, do = packed_inputs(cu[-1], Hq, Hkv, D, BF, seed=3)
+    cu_dev, max_len = ops.cu_seqlens_ready(torch.tensor(cu), cu[-1], q.device)
+    o, lse = ops.forward_varlen(q, k, v, cu_dev, max_len, W, S, 0.125)
+    dq, dk, dv = ops.backward_varlen(q, k, v, o, lse, do, cu_dev, max_len, W, S, 0.125)
+    for lo, hi in zip(cu[:-1], cu[1:]):
+        as4 = lambda t: t[lo:hi].permute(1, 0, 2).unsqueeze(0)
+        o1, lse1 = ops.forward(as4(q), as4(k), as4(v), W, S, 0.125)
+        dq1, dk1, dv1 = ops.backward(as4(q), as4(k), as4(v), o1, lse1, as4(do), W, S, 0.125)
+        assert torch.equal(as4(o), o1)
+        assert torch.equal(lse[:, lo:hi], lse1[0])
+        assert torch.equal(as4(dq), dq1)
+        assert torch.allclose(as4(dk).float(), dk1.float(), atol=2e-2, rtol=1e-2)
+        assert torch.allclose(as4(dv).float(), dv1.float(), atol=2e-2, rtol=1e-2)
+
+
+def test_varlen_autograd_api_and_determinism(gpu):
+    fa = load_pkg()
+    cu = torch.tensor([0, 300, 301, 900], dtype=torch.int32)
+    q, k, v, do = packed_inputs(900, 8, 2, 64, BF, seed=4)
+    runs = []
+    for cu_arg, max_len in ((cu, None), (cu.cuda(), 600)):
+        qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+        o = fa.flash_swda_with_sink_varlen(qg, kg, vg, cu_arg, max_len, 128, 4)
+        o.backward(do)
+        runs.append((o.detach(), qg.grad, kg.grad, vg.grad))
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    ops = load_mod("_ops")
+    ref = ops.forward_varlen(q, k, v, cu.cuda(), 600, 128, 4, 1 / 8)[0]
+    assert torch.equal(runs[0][0], ref)
+
+
+def test_varlen_argument_errors(gpu):
+    fa = load_pkg()
+    q, k, v, _ = packed_inputs(100, 4, 2, 64, BF, seed=1)
+    with pytest.raises(ValueError, match="non-decreasing"):
+        fa.flash_swda_with_sink_varlen(q, k, v, torch.tensor([0, 60, 50, 100]), None, 16, 1)
+    with pytest.raises(ValueError, match="number of packed rows"):
+        fa.flash_swda_with_sink_varlen(q, k, v, torch.tensor([0, 60, 120]), None, 16, 1)
+    with pytest.raises(ValueError, match="max_seqlen is required"):
+        fa.flash_swda_with_sink_varlen(q, k, v, torch.tensor([0, 100], dtype=torch.int32).cuda(), None, 16, 1)
+    with pytest.raises(ValueError, match="below the longest"):
+        fa.flash_swda_with_sink_varlen(q, k, v, torch.tensor([0, 100]), 50, 16, 1)
