@@ -224,6 +224,46 @@ def time_steps(fa, cfg, q, k, v, do, steps, warmup):
     return dict(fwdbwd_ms=fb_ms, fwdbwd_event_ms=fb_event_ms, fwd_ms=f_ms, bwd_ms=b_ms, peak_mem_gb=peak_gb)
 
 
+VARLEN_SEQS = (4096, 2048, 1024, 512, 3000, 1500, 700, 3504)  # 16384 packed rows
+
+
+def varlen_measure(steps, warmup, seqs=VARLEN_SEQS):
+    """fwd + bwd of a packed batch of GPT-OSS sliding-layer sequences of mixed lengths (Hq = 64,
+    Hkv = 8, D = 64, W = 128, S = 4, bf16) through flash_swda_with_sink_varlen, cu_seqlens on the
+    device; useful FLOPs count each sequence's allowed pairs."""
+    import torch
+
+    fa = _pkg()
+    flops_mod = _mod("flops")
+    Hq, Hkv, D, W, S = 64, 8, 64, 128, 4
+    total = sum(seqs)
+    g = torch.Generator().manual_seed(0)
+    dev = torch.device("cuda", 0)
+    q, k, v, do = (torch.randn(total, h, D, generator=g).to(torch.bfloat16).to(dev) for h in (Hq, Hkv, Hkv, Hq))
+    cu = torch.tensor([0] + list(__import__("itertools").accumulate(seqs)), dtype=torch.int32, device=dev)
+    qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+
+    def step():
+        qg.grad = kg.grad = vg.grad = None
+        o = fa.flash_swda_with_sink_varlen(qg, kg, vg, cu, max(seqs), W, S)
+        o.backward(do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = sum(14.0 * D * flops_mod.allowed_pairs_per_head(L, W, S) * Hq for L in seqs)
+    return {"workload": f"packed batch of {len(seqs)} sequences ({', '.join(map(str, seqs))}; {total} rows), "
+                        f"Hq={Hq} Hkv={Hkv} D={D} W={W} S={S} bf16, fwd+bwd", "ms_per_step": round(ms, 4),
+            "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s"}
+
+
 def sdpa_baseline(cfg, q, k, v, do, steps=10, warmup=3):
     """PyTorch-ROCm SDPA with a boolean mask, the reference's second baseline
     (pytorch_sdpa_attention, benchmark_backward_speed.py:57-65), fwd + autograd bwd on the GPU in
@@ -409,6 +449,8 @@ def main():
         "kernels": kernels,
         "roofline": roofline,
     }
+    if args.config == "c2":
+        line["varlen"] = varlen_measure(args.steps, args.warmup)
     if not args.no_sdpa_baseline:
         line["sdpa_baseline"] = sdpa_baseline(cfg, q, k, v, do)
     if not args.no_cpu_baseline:

@@ -88,16 +88,22 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
     int b, kvh, hw, q0, qw, L;
     int64_t row;
   };
+  // Tile order, slowest first: KV head, batch, head group of the KV head, row tile -- the tiles of
+  // one (batch, KV head) are contiguous, tiles_per_kv of them starting at (b + B kvh) tiles_per_kv.
+  // The KV head is outermost so that the XCD ranges split over KV heads before they split over
+  // sequences: with at least 8 KV heads every XCD gets the same sequences, so the work stays even
+  // when the sequences of a variable-length batch differ in length.
   auto decode = [&](int tile) {
     TileIdx t;
     const int qt = tile % a.n_qtiles, hg = tile / a.n_qtiles;
-    const int groups_per_batch = a.Hq / a.wh;
-    t.b = hg / groups_per_batch;
+    const int gpk = a.G / a.wh;  // head groups per KV head
+    const int bk = hg / gpk;
+    t.b = bk % a.B;
+    t.kvh = bk / a.B;
     const Seq sq = seq_of(a, t.b);
     t.L = sq.L;
     t.row = sq.row;
-    const int h0 = (hg % groups_per_batch) * a.wh;
-    t.kvh = h0 / a.G;
+    const int h0 = t.kvh * a.G + (hg % gpk) * a.wh;
     t.q0 = qt * 32 * a.wq;
     t.qw = t.q0 + 32 * (wave % a.wq);
     t.hw = h0 + wave / a.wq;
@@ -239,9 +245,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
       }
     };
 
-    gload(qplan_block(plan, 0));
-    sstore(0);
-    __syncthreads();
+    if (plan.nb > 0) {  // (a tile past its sequence's end, in a variable-length batch, has none)
+      gload(qplan_block(plan, 0));
+      sstore(0);
+      __syncthreads();
+    }
 
     for (int i = 0; i < plan.nb; ++i) {
       const int kb = qplan_block(plan, i);
@@ -456,8 +464,10 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
   // workgroups run last, filling the slots that the regular ones leave.
   const int per_group = a.n_kblocks + a.nsp * a.n_chunks;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
+  // groups in (KV head, batch) order, the KV head outermost: the XCDs then split over KV heads
+  // before sequences, which keeps their work even for sequences of different lengths
   const int grp = id / per_group, r = id % per_group;
-  const int kvh = grp % a.Hkv, b = grp / a.Hkv;
+  const int kvh = grp / a.B, b = grp % a.B;
   const Seq sq = seq_of(a, b);
   const int L = sq.L;
   int kblk, chunk = -1, qlo, qhi;
@@ -815,18 +825,19 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
     }
   }
   if (a.sink_dq) {
-    // The dQ kernel's flushed partials of this (b, KV head) = tiles [bh tpk, (bh + 1) tpk): on
+    // The dQ kernel's flushed partials of this (b, KV head) = tiles [(b + B kvh) tpk, + tpk): on
     // XCD x, whose tiles are [x_lo, x_hi) and whose a.dq_wgs / 8 workgroups stride through them,
     // the runs start at the first a.dq_wgs / 8 tiles of [max(x_lo, lo), min(x_hi, hi)).  All the
     // loads are independent; slots are added in (XCD, tile) order.
+    constexpr int nx = 8;
     const int tpk = a.n_qtiles * (a.G / a.wh);
     const int n_tiles = tpk * a.B * a.Hkv;
-    const int wgs_x = a.dq_wgs / 8;
-    const int lo = bh * tpk, hi = lo + tpk;
-    const int per = n_tiles / 8, rem = n_tiles % 8;
+    const int wgs_x = a.dq_wgs / nx;
+    const int lo = (b + a.B * kvh) * tpk, hi = lo + tpk;
+    const int per = n_tiles / nx, rem = n_tiles % nx;
     const int n_out = 2 * a.srows * D;
     const float* dsrc = a.dq_sink_part + row * D + d;
-    for (int x = 0; x < 8; ++x) {
+    for (int x = 0; x < nx; ++x) {
       const int x_lo = x * per + min(x, rem), x_hi = x_lo + per + (x < rem ? 1 : 0);
       const int A = max(x_lo, lo), B = min(x_hi, hi);
       const int n = B > A ? min(wgs_x, B - A) : 0;

@@ -193,8 +193,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // this workgroup's tiles: its XCD's contiguous range [t_lo, t_hi), from pos with stride
   // wgs_x (neighbouring tiles share K/V rows in that XCD's L2)
   const int hwg = HPW * a.wh;
-  const int groups_per_batch = a.Hq / hwg;
-  const int n_tiles = a.n_qtiles * a.B * groups_per_batch;
+  const int n_tiles = a.n_qtiles * a.B * (a.Hq / hwg);
   const int xcd = blockIdx.x % NX, pos = blockIdx.x / NX, wgs_x = gridDim.x / NX;
   const int per = n_tiles / NX, rem = n_tiles % NX;
   const int t_lo = xcd * per + min(xcd, rem), t_hi = t_lo + per + (xcd < rem ? 1 : 0);
@@ -205,15 +204,21 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     int b, kvh, hw, q0, qw, L;
     int64_t row;
   };
+  // Tile order, slowest first: KV head, batch, head group of the KV head, row tile.  The KV head
+  // is outermost so that the XCD ranges split over KV heads before they split over sequences:
+  // with at least 8 KV heads every XCD gets the same sequences, so the work stays even when the
+  // sequences of a variable-length batch differ in length (their tiles past the end are empty).
   auto decode = [&](int tile) {
     TileIdx t;
     const int qt = tile % a.n_qtiles, hg = tile / a.n_qtiles;
-    t.b = hg / groups_per_batch;
+    const int gpk = a.G / hwg;  // head groups per KV head
+    const int bk = hg / gpk;
+    t.b = bk % a.B;
+    t.kvh = bk / a.B;
     const Seq sq = seq_of(a, t.b);
     t.L = sq.L;
     t.row = sq.row;
-    const int h0 = (hg % groups_per_batch) * hwg;
-    t.kvh = h0 / a.G;
+    const int h0 = t.kvh * a.G + (hg % gpk) * hwg;
     t.q0 = qt * 32 * a.wq;
     t.qw = t.q0 + 32 * (wave % a.wq);
     t.hw = h0 + HPW * (wave / a.wq);
@@ -326,9 +331,11 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     }
   };
 
-  gload(qplan_block(plan, 0));
-  sstore(0);
-  __syncthreads();
+  if (plan.nb > 0) {  // (a tile past its sequence's end, in a variable-length batch, has none)
+    gload(qplan_block(plan, 0));
+    sstore(0);
+    __syncthreads();
+  }
 
   for (int i = 0; i < plan.nb; ++i) {
     const int kb = qplan_block(plan, i);
