@@ -65,7 +65,8 @@ struct Seq {
   int64_t row;
 };
 
-__device__ __forceinline__ Seq seq_of(const Args& a, int b) {
+template <typename A>
+__device__ __forceinline__ Seq seq_of(const A& a, int b) {
   if (!a.cu_seqlens) return Seq{a.L, 0};
   int lo = a.cu_seqlens[b], hi = a.cu_seqlens[b + 1];
   lo = lo < 0 ? 0 : (lo > a.total_rows ? a.total_rows : lo);
@@ -74,10 +75,30 @@ __device__ __forceinline__ Seq seq_of(const Args& a, int b) {
   return Seq{n < a.L ? n : a.L, lo};
 }
 
-// Element offset of row `row` of (batch b, head h) of a tensor with strides s[3].
-__device__ __forceinline__ int64_t slice_off(const int64_t s[3], int b, int h, int64_t row) {
+// Element offset of row `row` of (batch b, head h) of a tensor with strides s[3] (a plain array
+// or one read through args_fresh()).
+template <typename S3>
+__device__ __forceinline__ int64_t slice_off(const S3& s, int b, int h, int64_t row) {
   return int64_t(b) * s[0] + int64_t(h) * s[1] + row * s[2];
 }
+
+#if defined(__HIP_DEVICE_COMPILE__)
+// The kernel's Args in the kernarg segment (constant address space), re-read at the point of
+// use.  Fields read through the by-value parameter are loaded once at kernel entry and stay in
+// scalar registers for the whole kernel; the many pointers and 64-bit strides that only the
+// per-tile address arithmetic needs then spill scalar registers into vector lanes inside the key
+// loops.  The empty asm hides where the pointer comes from, so the loads through each call's
+// result are issued after the call, where the fields are used (scalar-cache hits).
+using KArgs = const __attribute__((address_space(4))) Args;
+__device__ __forceinline__ KArgs& args_fresh() {
+  KArgs* p = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return *p;
+}
+#else
+using KArgs = const Args;
+__device__ KArgs& args_fresh();  // device code only
+#endif
 
 // Launchers (return the hipError_t of the launch; launch_bwd_dkdv also launches the sink fold).
 hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stream);

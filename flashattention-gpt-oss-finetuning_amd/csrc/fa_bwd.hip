@@ -94,19 +94,20 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   // sequences: with at least 8 KV heads every XCD gets the same sequences, so the work stays even
   // when the sequences of a variable-length batch differ in length.
   auto decode = [&](int tile) {
+    KArgs& A = args_fresh();
     TileIdx t;
-    const int qt = tile % a.n_qtiles, hg = tile / a.n_qtiles;
-    const int gpk = a.G / a.wh;  // head groups per KV head
+    const int qt = tile % A.n_qtiles, hg = tile / A.n_qtiles;
+    const int gpk = A.G / A.wh;  // head groups per KV head
     const int bk = hg / gpk;
-    t.b = bk % a.B;
-    t.kvh = bk / a.B;
-    const Seq sq = seq_of(a, t.b);
+    t.b = bk % A.B;
+    t.kvh = bk / A.B;
+    const Seq sq = seq_of(A, t.b);
     t.L = sq.L;
     t.row = sq.row;
-    const int h0 = t.kvh * a.G + (hg % gpk) * a.wh;
-    t.q0 = qt * 32 * a.wq;
-    t.qw = t.q0 + 32 * (wave % a.wq);
-    t.hw = h0 + wave / a.wq;
+    const int h0 = t.kvh * A.G + (hg % gpk) * A.wh;
+    t.q0 = qt * 32 * A.wq;
+    t.qw = t.q0 + 32 * (wave % A.wq);
+    t.hw = h0 + wave / A.wq;
     return t;
   };
 
@@ -118,22 +119,25 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   uint16_t* stash = lds + 2 * BUF + wave * STASH;
   constexpr int CPR = D / 8;  // 16-byte chunks per row
   auto stash_rows = [&](const TileIdx& t) {
-    const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(a.q) + 2 * slice_off(a.sq, t.b, t.hw, t.row), span_bytes(t.L, a.sq[2], D));
-    const rsrc_t rd = make_rsrc(reinterpret_cast<const char*>(a.dout) + 2 * slice_off(a.sdo, t.b, t.hw, t.row), span_bytes(t.L, a.sdo[2], D));
-    const rsrc_t ro = make_rsrc(reinterpret_cast<const char*>(a.o) + 2 * slice_off(a.so, t.b, t.hw, t.row), span_bytes(t.L, a.so[2], D));
+    KArgs& A = args_fresh();
+    const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(A.q) + 2 * slice_off(A.sq, t.b, t.hw, t.row), span_bytes(t.L, A.sq[2], D));
+    const rsrc_t rd = make_rsrc(reinterpret_cast<const char*>(A.dout) + 2 * slice_off(A.sdo, t.b, t.hw, t.row), span_bytes(t.L, A.sdo[2], D));
+    const rsrc_t ro = make_rsrc(reinterpret_cast<const char*>(A.o) + 2 * slice_off(A.so, t.b, t.hw, t.row), span_bytes(t.L, A.so[2], D));
+    const int64_t sq2 = A.sq[2], sdo2 = A.sdo[2], so2 = A.so[2];
 #pragma unroll
     for (int p = 0; p < KS; ++p) {
       const int tr = (64 * p + lane) / CPR;  // tile row of this lane's 16-byte position
       const int col = 8 * (((64 * p + lane) % CPR) ^ swz<D>(tr));
       const int64_t row = t.qw + tr;
-      buf_dma16(rq, stash + 0 * TILE + 512 * p, uint32_t((row * a.sq[2] + col) * 2));
-      buf_dma16(rd, stash + 1 * TILE + 512 * p, uint32_t((row * a.sdo[2] + col) * 2));
-      buf_dma16(ro, stash + 2 * TILE + 512 * p, uint32_t((row * a.so[2] + col) * 2));
+      buf_dma16(rq, stash + 0 * TILE + 512 * p, uint32_t((row * sq2 + col) * 2));
+      buf_dma16(rd, stash + 1 * TILE + 512 * p, uint32_t((row * sdo2 + col) * 2));
+      buf_dma16(ro, stash + 2 * TILE + 512 * p, uint32_t((row * so2 + col) * 2));
     }
   };
   auto load_lse = [&](const TileIdx& t) {
-    const rsrc_t rl = make_rsrc(a.lse + slice_off(a.slse, t.b, t.hw, t.row), span_f32(t.L, a.slse[2]));
-    return buf_ldf(rl, uint32_t(int64_t(t.qw + r32) * a.slse[2] * 4));
+    KArgs& A = args_fresh();
+    const rsrc_t rl = make_rsrc(A.lse + slice_off(A.slse, t.b, t.hw, t.row), span_f32(t.L, A.slse[2]));
+    return buf_ldf(rl, uint32_t(int64_t(t.qw + r32) * A.slse[2] * 4));
   };
 
   // K/V staging offsets (the same for every tile)
@@ -188,19 +192,22 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
       const int off = swz_off<D>(r32, hf * (D / 2) + 8 * ks);
       qf[ks] = lds16(Qs + off) ^ a.qsign;
       dof[ks] = lds16(Ds + off);
-      dsum += dot8<E>(dof[ks], lds16(Os + off));
+      dsum = dot8<E>(dof[ks], lds16(Os + off), dsum);
     }
     const float delta = sum_halves(dsum);
     const float ndelta = -delta;
     const float lse2 = q < L ? lse_next * kLog2e : __builtin_inff();
-    if (q < L && hf == 0) a.delta[(int64_t(t.b) * a.Hq + t.hw) * a.Lp + q] = delta;
-    if (a.sink_logits && wave_active) {
-      // learned sink: d sink = -sum over rows of P_sink * delta, P_sink = 2^(sink*log2e - lse2);
-      // one partial per 32-row block, summed in a fixed order by bwd_sink_logit_kernel
-      float v = q < L ? fast_exp2(a.sink_logits[t.hw] * kLog2e - lse2) * delta : 0.f;
+    {
+      KArgs& A = args_fresh();
+      if (q < L && hf == 0) A.delta[(int64_t(t.b) * A.Hq + t.hw) * A.Lp + q] = delta;
+      if (A.sink_logits && wave_active) {
+        // learned sink: d sink = -sum over rows of P_sink * delta, P_sink = 2^(sink*log2e - lse2);
+        // one partial per 32-row block, summed in a fixed order by bwd_sink_logit_kernel
+        float v = q < L ? fast_exp2(A.sink_logits[t.hw] * kLog2e - lse2) * delta : 0.f;
 #pragma unroll
-      for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-      if (lane == 0) a.dsink_part[(int64_t(t.b) * a.Hq + t.hw) * (a.Lp / 32) + qw / 32] = -v;
+        for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+        if (lane == 0) A.dsink_part[(int64_t(t.b) * A.Hq + t.hw) * (A.Lp / 32) + qw / 32] = -v;
+      }
     }
     // this wave's rows add to the sink keys' gradients (rows past key block 0's window)
     const int sink_row0 = dq_sink_row0(L, W);
@@ -211,8 +218,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
     for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
 
     const QPlan plan = qplan(t.q0, 32 * a.wq, L, W, S);
-    const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * slice_off(a.sk, t.b, t.kvh, t.row), span_bytes(L, a.sk[2], D));
-    const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * slice_off(a.sv, t.b, t.kvh, t.row), span_bytes(L, a.sv[2], D));
+    KArgs& Akv = args_fresh();
+    const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(Akv.k) + 2 * slice_off(Akv.sk, t.b, t.kvh, t.row), span_bytes(L, Akv.sk[2], D));
+    const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(Akv.v) + 2 * slice_off(Akv.sv, t.b, t.kvh, t.row), span_bytes(L, Akv.sv[2], D));
     u32x4 kreg[NK], vreg[NK];
     auto gload = [&](int kb) {
 #pragma unroll
@@ -368,13 +376,15 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     if (wave_active && q < L) {
-      char* dqp = reinterpret_cast<char*>(a.dq) + 2 * slice_off(a.sdq, t.b, t.hw, t.row + q);
+      KArgs& A = args_fresh();
+      char* dqp = reinterpret_cast<char*>(A.dq) + 2 * slice_off(A.sdq, t.b, t.hw, t.row + q);
+      const float scale = A.scale;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         if (D == 16 && hf == 1) continue;
         float v[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) v[e] = acc[db][e] * a.scale;
+        for (int e = 0; e < 16; ++e) v[e] = acc[db][e] * scale;
         const int d0 = 32 * db + (D >= 32 ? 16 * hf : 0);
         st16(dqp + 2 * d0, pack8<E>(v));
         st16(dqp + 2 * (d0 + 8), pack8<E>(v + 8));
@@ -390,7 +400,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
       // which is how bwd_sink_fold_kernel finds the slots.
       const bool flush = !has_next || (tile + wgs_x) / tiles_per_kv != tile / tiles_per_kv;
       if (flush) {
-        const int sr = a.srows;
+        KArgs& A = args_fresh();
+        const int sr = A.srows;
         float* red = reinterpret_cast<float*>(lds);
         const int g4 = lane >> 4, i16 = lane & 15;
 #pragma unroll
@@ -405,7 +416,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
           }
         __syncthreads();
         const int n_out = 2 * sr * D;
-        float* slot = a.dq_sink_part + int64_t(run_first) * n_out;
+        float* slot = A.dq_sink_part + int64_t(run_first) * n_out;
         run_first = tile + wgs_x;
         for (int x = tid; x < n_out; x += 256) {
           const int kind = x / (sr * D), rest = x % (sr * D);

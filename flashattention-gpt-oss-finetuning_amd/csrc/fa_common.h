@@ -64,6 +64,11 @@ struct BF16 {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
                                            __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
   }
+  // acc + a.lo * b.lo + a.hi * b.hi of two packed pairs (v_dot2, fp32 accumulation)
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc,
+                                           false);
+  }
 };
 
 struct F16 {
@@ -86,6 +91,9 @@ struct F16 {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), __builtin_bit_cast(f16x2, 0x3c003c00u), acc,
                                   false);
   }
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);
+  }
 };
 
 // Eight fp32 C values -> one 16-byte B operand.
@@ -99,16 +107,13 @@ __device__ __forceinline__ u32x4 pack8(const float* x) {
   return r;
 }
 
-// Dot product of two 16-byte vectors of 16-bit values, accumulated in fp32.
+// acc + the dot product of two 16-byte vectors of 16-bit values, accumulated in fp32 (four
+// v_dot2 instructions).
 template <typename E>
-__device__ __forceinline__ float dot8(u32x4 a, u32x4 b) {
-  float s = 0.f;
+__device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    s += E::to_f32(uint16_t(a[w])) * E::to_f32(uint16_t(b[w]));
-    s += E::to_f32(uint16_t(a[w] >> 16)) * E::to_f32(uint16_t(b[w] >> 16));
-  }
-  return s;
+  for (int w = 0; w < 4; ++w) acc = E::dot2(a[w], b[w], acc);
+  return acc;
 }
 
 // Storage position of index r (0..15) inside a 16-group of a "permuted" LDS row: the middle

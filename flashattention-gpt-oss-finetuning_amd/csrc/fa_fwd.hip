@@ -209,19 +209,20 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // with at least 8 KV heads every XCD gets the same sequences, so the work stays even when the
   // sequences of a variable-length batch differ in length (their tiles past the end are empty).
   auto decode = [&](int tile) {
+    KArgs& A = args_fresh();
     TileIdx t;
-    const int qt = tile % a.n_qtiles, hg = tile / a.n_qtiles;
-    const int gpk = a.G / hwg;  // head groups per KV head
+    const int qt = tile % A.n_qtiles, hg = tile / A.n_qtiles;
+    const int gpk = A.G / hwg;  // head groups per KV head
     const int bk = hg / gpk;
-    t.b = bk % a.B;
-    t.kvh = bk / a.B;
-    const Seq sq = seq_of(a, t.b);
+    t.b = bk % A.B;
+    t.kvh = bk / A.B;
+    const Seq sq = seq_of(A, t.b);
     t.L = sq.L;
     t.row = sq.row;
-    const int h0 = t.kvh * a.G + (hg % gpk) * hwg;
-    t.q0 = qt * 32 * a.wq;
-    t.qw = t.q0 + 32 * (wave % a.wq);
-    t.hw = h0 + HPW * (wave / a.wq);
+    const int h0 = t.kvh * A.G + (hg % gpk) * hwg;
+    t.q0 = qt * 32 * A.wq;
+    t.qw = t.q0 + 32 * (wave % A.wq);
+    t.hw = h0 + HPW * (wave / A.wq);
     return t;
   };
 
@@ -231,11 +232,12 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // read as zero.
   uint16_t* stash = lds + 2 * BUF + wave * STASH;
   auto q_rsrc = [&](const TileIdx& t, int h) {
-    return make_rsrc(reinterpret_cast<const char*>(a.q) + 2 * slice_off(a.sq, t.b, t.hw + h, t.row),
-                     span_bytes(t.L, a.sq[2], D));
+    KArgs& A = args_fresh();
+    return make_rsrc(reinterpret_cast<const char*>(A.q) + 2 * slice_off(A.sq, t.b, t.hw + h, t.row),
+                     span_bytes(t.L, A.sq[2], D));
   };
   auto q_off = [&](const TileIdx& t, int ks) {
-    return uint32_t((int64_t(t.qw + r32) * a.sq[2] + hf * (D / 2) + 8 * ks) * 2);
+    return uint32_t((int64_t(t.qw + r32) * args_fresh().sq[2] + hf * (D / 2) + 8 * ks) * 2);
   };
   auto stash_rows = [&](const TileIdx& t) {
 #pragma unroll
@@ -303,10 +305,11 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
 
   // K/V of the KV head through buffer resources spanning the sequence's rows [0, L): rows past L
   // read as zero, so the loads need no branches (a slice is < 2^31 bytes, checked by the C ABI).
-  const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * slice_off(a.sk, b, kvh, t.row),
-                              span_bytes(L, a.sk[2], D));
-  const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * slice_off(a.sv, b, kvh, t.row),
-                              span_bytes(L, a.sv[2], D));
+  KArgs& Akv = args_fresh();
+  const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(Akv.k) + 2 * slice_off(Akv.sk, b, kvh, t.row),
+                              span_bytes(L, Akv.sk[2], D));
+  const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(Akv.v) + 2 * slice_off(Akv.sv, b, kvh, t.row),
+                              span_bytes(L, Akv.sv[2], D));
 
   // Register staging of the next LDS block.
   u32x4 kreg[NK], vreg[NK];
@@ -373,17 +376,18 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     float lt = sum_halves(lsum[h]);
     if (q >= L) continue;
     float mt = m2[h], r = 1.f;
-    if (a.sink_logits) {
+    KArgs& A = args_fresh();
+    if (A.sink_logits) {
       // the learned sink joins the denominator: l' = l 2^(m - m') + 2^(sink*log2e - m'), with
       // m' = max(m, sink*log2e) so that neither term overflows
-      const float sl = a.sink_logits[hw + h] * kLog2e;
+      const float sl = A.sink_logits[hw + h] * kLog2e;
       const float mn = fmaxf(mt, sl);
       r = fast_exp2(mt - mn);
       lt = lt * r + fast_exp2(sl - mn);
       mt = mn;
     }
     const float inv = lt > 0.f ? r / lt : 0.f;
-    char* op = reinterpret_cast<char*>(a.o_out) + 2 * slice_off(a.so_out, b, hw + h, t.row + q);
+    char* op = reinterpret_cast<char*>(A.o_out) + 2 * slice_off(A.so_out, b, hw + h, t.row + q);
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       if (D == 16 && hf == 1) continue;
@@ -395,7 +399,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
       st16(op + 2 * (d0 + 8), pack8<E>(ov + 8));
     }
     if (hf == 0) {
-      a.lse_out[slice_off(a.slse, b, hw + h, t.row + q)] =
+      A.lse_out[slice_off(A.slse, b, hw + h, t.row + q)] =
           (mt + fast_log2(lt)) * kLn2;
     }
   }
