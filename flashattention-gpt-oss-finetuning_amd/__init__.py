@@ -9,6 +9,11 @@ Variable-length (packed) batches, q [total, Hq, D] with cu_seqlens [B + 1]:
     flash_swda_with_sink_varlen(q, k, v, cu_seqlens, max_seqlen, window_size, sink_size=0,
                                 scale=None, sinks=None)
 
+FP8 (OCP e4m3) forward for the compute-bound shapes, D in {64, 128}, o in bfloat16:
+    q8, qd = quantize_fp8(q); ...
+    flash_swda_with_sink_fp8(q8, k8, v8, window_size, sink_size=0, scale=None,
+                             descale=(qd, kd, vd), sinks=None)
+
 GPT-OSS integration (gpt_oss.py): learned per-head sink logits, [B, L, H, D] tensors, full and
 sliding layers, and transformers' attention-function interface:
     attention(q, k, v, window_size=None, sink_size=0, sinks=None, scale=None, layout="bhld")
@@ -19,7 +24,8 @@ The directory name is not a Python identifier; import it with
 ``importlib.import_module("flashattention-gpt-oss-finetuning_amd")`` from the repository root.
 """
 from .attention import (FlashSWDAWithLearnedSinks, FlashSWDAWithSink, FlashSWDAWithSinkVarlen,  # noqa: F401
-                        flash_swda_with_sink, flash_swda_with_sink_varlen, swa_sink_attention)
+                        flash_swda_with_sink, flash_swda_with_sink_fp8, flash_swda_with_sink_varlen,
+                        quantize_fp8, swa_sink_attention)
 from .gpt_oss import attention, gpt_oss_attention_forward, register_transformers  # noqa: F401
 from .flops import Workload, allowed_pairs_per_head  # noqa: F401
 
@@ -30,6 +36,8 @@ __all__ = [
     "FlashSWDAWithLearnedSinks",
     "FlashSWDAWithSinkVarlen",
     "flash_swda_with_sink_varlen",
+    "flash_swda_with_sink_fp8",
+    "quantize_fp8",
     "attention",
     "gpt_oss_attention_forward",
     "register_transformers",

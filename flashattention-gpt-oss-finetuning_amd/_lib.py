@@ -17,6 +17,7 @@ HEADER_PATH = os.path.join(os.path.dirname(PKG_DIR), "include", "fa_gfx950.h")
 
 FA_DTYPE_BF16 = 1
 FA_DTYPE_F16 = 2
+FA_DTYPE_FP8_E4M3 = 3
 
 FA_OK = 0
 FA_ERR_NULL = -1
@@ -40,6 +41,7 @@ EXPORTS = (
     "fa_bwd_sinks",
     "fa_fwd_varlen",
     "fa_bwd_varlen",
+    "fa_fwd_fp8",
     "fa_bwd_workspace_bytes",
     "fa_check_fwd",
     "fa_check_bwd",
@@ -139,6 +141,9 @@ def lib() -> ctypes.CDLL:
             L.fa_bwd_varlen.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p,
                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
             L.fa_bwd_varlen.restype = ctypes.c_int
+            L.fa_fwd_fp8.argtypes = [ctypes.POINTER(FwdParams), ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                     ctypes.c_void_p, ctypes.c_void_p]
+            L.fa_fwd_fp8.restype = ctypes.c_int
             L.fa_bwd_workspace_bytes.argtypes = [ctypes.c_int32] * 7
             L.fa_bwd_workspace_bytes.restype = ctypes.c_size_t
             L.fa_check_fwd.argtypes = [ctypes.POINTER(FwdParams)]

@@ -166,6 +166,76 @@ def forward(q, k, v, window: int, sink: int, scale: float, sinks=None):
     return call.o, call.lse
 
 
+def _fp8_ready(t: torch.Tensor) -> torch.Tensor:
+    """e4m3 inputs as fa_fwd_fp8 reads them: head-dim stride 1, strides multiples of 16 elements
+    (bytes), 16-byte aligned base; otherwise a contiguous copy."""
+    st = t.stride()
+    if st[3] != 1 or (t.data_ptr() & 15) or (st[0] & 15) or (st[1] & 15) or (st[2] & 15):
+        t = t.contiguous()
+        if t.data_ptr() & 15:
+            t = t.clone(memory_format=torch.contiguous_format)
+    return t
+
+
+class Fp8FwdCall:
+    """A prepared fa_fwd_fp8 launch: q [B,Hq,L,D], k/v [B,Hkv,L,D] in torch.float8_e4m3fn standing
+    for descale[i] times their values; o is bfloat16 with q's memory layout, lse float32 [B,Hq,L]."""
+
+    __slots__ = ("params", "inputs", "o", "lse", "device", "sinks", "descale")
+
+    def __init__(self, q, k, v, window: int, sink: int, scale: float, descale=(1.0, 1.0, 1.0), sinks=None):
+        dev = q.device
+        if dev.type != "cuda":
+            raise RuntimeError(f"q is on {dev}: the gfx950 attention kernels need GPU tensors "
+                               "(there is no CPU implementation)")
+        for t, n in ((q, "q"), (k, "k"), (v, "v")):
+            if t.dtype != torch.float8_e4m3fn:
+                raise ValueError(f"{n} has dtype {t.dtype}; the fp8 forward takes torch.float8_e4m3fn")
+            if t.dim() != 4:
+                raise ValueError(f"{n} must be 4-D [B, H, L, D], got shape {tuple(t.shape)}")
+            if t.device != dev:
+                raise RuntimeError(f"{n} is on {t.device} but q is on {dev}")
+        q, k, v = _fp8_ready(q), _fp8_ready(k), _fp8_ready(v)
+        B, Hq, L, D = q.shape
+        self.sinks = None if sinks is None else _sinks_ready(sinks, Hq, dev)
+        self.o = torch.empty_like(q, dtype=torch.bfloat16)
+        self.lse = torch.empty((B, Hq, L), dtype=torch.float32, device=dev)
+        self.inputs = (q, k, v)
+        self.device = dev
+        self.descale = tuple(float(x) for x in descale)
+        p = _lib.FwdParams()
+        p.q, p.k, p.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+        p.o, p.lse = self.o.data_ptr(), self.lse.data_ptr()
+        p.q_stride[:] = _strides3(q)
+        p.k_stride[:] = _strides3(k)
+        p.v_stride[:] = _strides3(v)
+        p.o_stride[:] = _strides3(self.o)
+        p.lse_stride[:] = self.lse.stride()
+        p.batch, p.heads_q, p.heads_kv, p.seqlen, p.head_dim = B, Hq, k.shape[1], L, D
+        p.window, p.sink = _i32(window), _i32(sink)
+        p.softmax_scale = scale
+        p.dtype = _lib.FA_DTYPE_FP8_E4M3
+        self.params = p
+
+    def run(self) -> None:
+        qd, kd, vd = self.descale
+        with _DeviceGuard(self.device):
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            rc = _lib.lib().fa_fwd_fp8(ctypes.byref(self.params), ctypes.c_float(qd), ctypes.c_float(kd),
+                                       ctypes.c_float(vd),
+                                       ctypes.c_void_p(None if self.sinks is None else self.sinks.data_ptr()),
+                                       ctypes.c_void_p(stream))
+        _lib.raise_for_status(rc, "fa_fwd_fp8")
+
+
+def forward_fp8(q, k, v, window: int, sink: int, scale: float, descale=(1.0, 1.0, 1.0), sinks=None):
+    """(o bf16, lse) of attention over the dequantised e4m3 inputs descale[0] q, descale[1] k,
+    descale[2] v (fa_fwd_fp8)."""
+    call = Fp8FwdCall(q, k, v, window, sink, scale, descale, sinks)
+    call.run()
+    return call.o, call.lse
+
+
 def workspace_bytes(B, Hq, Hkv, L, D, window, sink) -> int:
     return int(_lib.lib().fa_bwd_workspace_bytes(B, Hq, Hkv, L, D, _i32(window), _i32(sink)))
 

@@ -132,6 +132,38 @@ def flash_swda_with_sink_varlen(q, k, v, cu_seqlens, max_seqlen, window_size, si
     return FlashSWDAWithSinkVarlen.apply(q, k, v, cu_seqlens, max_seqlen, window_size, sink_size, scale, sinks)
 
 
+E4M3_MAX = 448.0  # largest finite float8 e4m3 (OCP) value
+
+
+def quantize_fp8(x: torch.Tensor, descale: Optional[float] = None):
+    """Per-tensor e4m3 quantisation for flash_swda_with_sink_fp8: returns (x8, descale) with
+    x ~= descale * x8 (x8 in torch.float8_e4m3fn, round to nearest even); descale defaults to
+    amax(|x|) / 448, so the largest magnitude maps to the largest finite e4m3 value."""
+    xf = x.detach().float()
+    if descale is None:
+        amax = float(xf.abs().max()) if xf.numel() else 0.0
+        descale = amax / E4M3_MAX if amax > 0.0 else 1.0
+    x8 = (xf / descale).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    return x8, float(descale)
+
+
+def flash_swda_with_sink_fp8(q, k, v, window_size, sink_size: int = 0, scale: Optional[float] = None,
+                             descale=(1.0, 1.0, 1.0), sinks=None):
+    """Forward only, FP8 inputs: q [B,Hq,L,D], k/v [B,Hkv,L,D] in torch.float8_e4m3fn standing for
+    descale[0] q, descale[1] k, descale[2] v (see quantize_fp8); D is 64 or 128.  Returns o in
+    bfloat16: the same attention (window, positional sinks, optional learned sink logits
+    `sinks` [Hq]) as flash_swda_with_sink on the dequantised inputs, with Q K^T on the fp8
+    matrix cores.  window_size None means full causal attention.  No autograd: the reference's
+    kernels have no fp8 path (flash_attention_gpt_oss.py:356-383 take 16/32-bit tensors)."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    _check_shapes(q, k, v)
+    if window_size is None:
+        window_size = q.shape[2]
+    o, _ = _ops.forward_fp8(q, k, v, int(window_size), int(sink_size), float(scale), descale, sinks)
+    return o
+
+
 def _check_shapes(q, k, v):
     """The shape conditions of flash_attention_gpt_oss.py:347-354, same messages."""
     if not (q.shape[0] == v.shape[0] and q.shape[2] == v.shape[2] and q.shape[3] == v.shape[3]):

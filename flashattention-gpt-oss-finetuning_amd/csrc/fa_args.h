@@ -36,6 +36,8 @@ struct Args {
   float scale;       // softmax scale as given
   float c;           // |scale| * log2(e), kept > 0: scores enter exp2 as s * c
   uint32_t qsign;    // 0x80008000 when scale < 0: flips the sign of Q in the score product
+                     // (0x80808080 for e4m3 inputs)
+  float oscale;      // forward with e4m3 inputs: O is multiplied by V's dequantisation factor
   // q-major kernels (forward, dQ): a workgroup is wq x wh waves, each wave 32 rows x HPW heads
   int wq, wh;
   int n_qtiles;
@@ -102,6 +104,7 @@ __device__ KArgs& args_fresh();  // device code only
 
 // Launchers (return the hipError_t of the launch; launch_bwd_dkdv also launches the sink fold).
 hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
+hipError_t launch_fwd_fp8(const Args& a, int D, int hpw, hipStream_t stream);  // e4m3 q, k, v; bf16 o
 hipError_t launch_bwd_dq(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
 hipError_t launch_bwd_dkdv(const Args& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_bwd_sink_logits(const Args& a, hipStream_t stream);  // after launch_bwd_dq

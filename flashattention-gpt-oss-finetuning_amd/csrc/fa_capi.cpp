@@ -20,9 +20,11 @@ constexpr int kChunkRows = 64;  // query rows per sink-chunk workgroup of the dK
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-bool strides_ok(const int64_t s[3]) {
+// strides in elements of `elem_bytes` bytes: non-negative and whole 16-byte multiples
+bool strides_ok(const int64_t s[3], int elem_bytes = 2) {
+  const int64_t m = 16 / elem_bytes - 1;
   for (int i = 0; i < 3; ++i)
-    if (s[i] < 0 || (s[i] & 7) != 0) return false;
+    if (s[i] < 0 || (s[i] & m) != 0) return false;
   return true;
 }
 
@@ -228,6 +230,55 @@ int run_fwd(const fa_fwd_params* p, const float* sinks, void* stream, const int3
   return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 
+// fa_fwd_fp8: e4m3 q, k, v (1-byte elements), bf16 o, D in {64, 128}, finite dequantisation factors.
+int check_fwd_fp8(const fa_fwd_params* p, float qd, float kd, float vd) {
+  if (!p) return FA_ERR_NULL;
+  if (!p->q || !p->k || !p->v || !p->o || !p->lse) return FA_ERR_NULL;
+  if (p->dtype != FA_DTYPE_FP8_E4M3) return FA_ERR_DTYPE;
+  const int rc = check_common(p->batch, p->heads_q, p->heads_kv, p->seqlen, p->head_dim, p->window, p->sink,
+                              p->softmax_scale, FA_DTYPE_BF16);
+  if (rc != FA_OK) return rc;
+  if (p->head_dim != 64 && p->head_dim != 128) return FA_ERR_HEAD_DIM;
+  if (!std::isfinite(qd) || !std::isfinite(kd) || !std::isfinite(vd) || !std::isfinite(p->softmax_scale * qd * kd))
+    return FA_ERR_SCALE;
+  if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o) || !aligned4(p->lse))
+    return FA_ERR_ALIGN;
+  if (!strides_ok(p->q_stride, 1) || !strides_ok(p->k_stride, 1) || !strides_ok(p->v_stride, 1) ||
+      !strides_ok(p->o_stride) || !lse_strides_ok(p->lse_stride))
+    return FA_ERR_ALIGN;
+  const int L = p->seqlen, D = p->head_dim;
+  if (!slice_fits(p->q_stride, L, D, 1) || !slice_fits(p->k_stride, L, D, 1) || !slice_fits(p->v_stride, L, D, 1))
+    return FA_ERR_OVERFLOW;
+  return FA_OK;
+}
+
+// The scores are (q_descale k_descale scale) * (q . k) over the stored e4m3 values; O is scaled
+// by v_descale in the kernel's epilogue.
+int run_fwd_fp8(const fa_fwd_params* p, float qd, float kd, float vd, const float* sinks, void* stream) {
+  const float scale = p->softmax_scale * qd * kd;
+  fa::Args a = base_args(p->batch, p->heads_q, p->heads_kv, p->seqlen, p->head_dim, p->window, p->sink, scale);
+  a.qsign = scale < 0.f ? 0x80808080u : 0u;
+  a.oscale = vd;
+  a.q = p->q;
+  a.k = p->k;
+  a.v = p->v;
+  a.o_out = p->o;
+  a.lse_out = p->lse;
+  a.sink_logits = sinks;
+  copy3(a.sq, p->q_stride);
+  copy3(a.sk, p->k_stride);
+  copy3(a.sv, p->v_stride);
+  copy3(a.so_out, p->o_stride);
+  copy3(a.slse, p->lse_stride);
+  int hpw, wh, wq;
+  choose_qmajor(a.G, p->head_dim == 64 ? 2 : 1, &hpw, &wh, &wq);
+  a.wh = wh;
+  a.wq = wq;
+  a.n_qtiles = (a.L + 32 * wq - 1) / (32 * wq);
+  const hipError_t e = fa::launch_fwd_fp8(a, p->head_dim, hpw, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+}
+
 }  // namespace
 
 extern "C" {
@@ -244,6 +295,14 @@ int fa_fwd_varlen(const fa_fwd_params* p, const int32_t* cu_seqlens, int32_t tot
   if (rc != FA_OK) return rc;
   if (sinks && !aligned4(sinks)) return FA_ERR_ALIGN;
   return run_fwd(p, sinks, stream, cu_seqlens, total_rows);
+}
+
+int fa_fwd_fp8(const fa_fwd_params* p, float q_descale, float k_descale, float v_descale, const float* sinks,
+               void* stream) {
+  const int rc = check_fwd_fp8(p, q_descale, k_descale, v_descale);
+  if (rc != FA_OK) return rc;
+  if (sinks && !aligned4(sinks)) return FA_ERR_ALIGN;
+  return run_fwd_fp8(p, q_descale, k_descale, v_descale, sinks, stream);
 }
 
 int fa_fwd_sinks(const fa_fwd_params* p, const float* sinks, void* stream) {
@@ -396,14 +455,14 @@ const char* fa_strerror(int status) {
     case FA_OK: return "ok";
     case FA_ERR_NULL: return "a required pointer is NULL";
     case FA_ERR_SHAPE: return "invalid shape: batch, heads and seqlen must be >= 1 and heads_q % heads_kv == 0";
-    case FA_ERR_HEAD_DIM: return "head_dim must be one of 16, 32, 64, 128";
-    case FA_ERR_DTYPE: return "dtype must be FA_DTYPE_BF16 or FA_DTYPE_F16";
-    case FA_ERR_ALIGN: return "tensors must be 16-byte aligned with non-negative strides that are multiples of 8 elements (lse: 4-byte aligned, non-negative strides)";
+    case FA_ERR_HEAD_DIM: return "head_dim must be one of 16, 32, 64, 128 (64 or 128 for fa_fwd_fp8)";
+    case FA_ERR_DTYPE: return "dtype must be FA_DTYPE_BF16 or FA_DTYPE_F16 (FA_DTYPE_FP8_E4M3 for fa_fwd_fp8)";
+    case FA_ERR_ALIGN: return "tensors must be 16-byte aligned with non-negative strides that are multiples of 16 bytes (lse: 4-byte aligned, non-negative strides)";
     case FA_ERR_MASK: return "window < 1 and sink < 1 leave every query row fully masked";
     case FA_ERR_WORKSPACE: return "workspace is NULL, not 256-byte aligned or smaller than fa_bwd_workspace_bytes()";
     case FA_ERR_LAUNCH: return "HIP kernel launch failed";
     case FA_ERR_OVERFLOW: return "problem size exceeds the kernels' index range";
-    case FA_ERR_SCALE: return "softmax_scale must be finite";
+    case FA_ERR_SCALE: return "softmax_scale (and the fp8 dequantisation factors) must be finite";
   }
   return "unknown fa_status";
 }

@@ -34,6 +34,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -96,6 +97,33 @@ struct F16 {
   }
 };
 
+// FP8 (OCP e4m3) operands.
+// v_mfma_scale_f32_32x32x64_f8f6f4 with unit block scales (E8M0 127 = 2^0): C += A B with A 32 x 64
+// and B 64 x 32 in e4m3; lane l supplies row l % 32 of A (column l % 32 of B) and the 32 bytes
+// [32 (l / 32), +32) of the K dimension, as two 16-byte halves (lo, hi); C is laid out as for
+// the 32x32 bf16 form (checked on hardware by an in-bounds probe against a CPU product).
+__device__ __forceinline__ f32x16 mfma_fp8(u32x4 a_lo, u32x4 a_hi, u32x4 b_lo, u32x4 b_hi, f32x16 c) {
+  const i32x8 a = {int(a_lo[0]), int(a_lo[1]), int(a_lo[2]), int(a_lo[3]),
+                   int(a_hi[0]), int(a_hi[1]), int(a_hi[2]), int(a_hi[3])};
+  const i32x8 b = {int(b_lo[0]), int(b_lo[1]), int(b_lo[2]), int(b_lo[3]),
+                   int(b_hi[0]), int(b_hi[1]), int(b_hi[2]), int(b_hi[3])};
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// Sixteen e4m3 values (16 bytes) -> sixteen bf16 (two 16-byte chunks, same order), exactly
+// (every finite e4m3 value is a bf16 value; v_cvt_scalef32_pk_bf16_fp8 with scale 1, checked on
+// hardware over all 256 byte values).
+__device__ __forceinline__ void fp8x16_to_bf16(u32x4 x, u32x4& lo, u32x4& hi) {
+  uint32_t o[8];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    o[2 * w] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x[w], 1.0f, false));
+    o[2 * w + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x[w], 1.0f, true));
+  }
+  lo = u32x4{o[0], o[1], o[2], o[3]};
+  hi = u32x4{o[4], o[5], o[6], o[7]};
+}
+
 // Eight fp32 C values -> one 16-byte B operand.
 template <typename E>
 __device__ __forceinline__ u32x4 pack8(const float* x) {
@@ -157,9 +185,10 @@ __device__ __forceinline__ void buf_dma16(rsrc_t r, uint16_t* lds_dst, uint32_t 
 __device__ __forceinline__ uint32_t span_f32(int rows, int64_t stride) {
   return rows > 0 ? uint32_t((int64_t(rows - 1) * stride + 1) * 4) : 0u;
 }
-// Bytes spanned by `rows` rows of `cols` 16-bit elements with row stride `stride` (0 if none).
-__device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride, int cols) {
-  return rows > 0 ? uint32_t((int64_t(rows - 1) * stride + cols) * 2) : 0u;
+// Bytes spanned by `rows` rows of `cols` elements of `eb` bytes (16-bit by default) with row
+// stride `stride` elements (0 if none).
+__device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride, int cols, int eb = 2) {
+  return rows > 0 ? uint32_t((int64_t(rows - 1) * stride + cols) * eb) : 0u;
 }
 
 // ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, output lane i, element j is

@@ -64,12 +64,18 @@ __device__ __forceinline__ void fwd_patterns(float* pat, int W, int S) {
   }
 }
 
-template <typename E, int D, int HPW>
+// Q fragments per head and lane: 16 bytes each, head-dim slice [hf*D/2 + 8ks, +8) for 16-bit
+// inputs; for e4m3 inputs, fragment f holds bytes [64 (f / 2) + 32 hf + 16 (f % 2), +16) of the
+// row, the operand layout of the fp8 MFMA.
+template <int D, bool F8>
+constexpr int kQFrags = F8 ? D / 32 : D / 16;
+
+template <typename E, int D, int HPW, bool F8>
 __device__ __forceinline__ void fwd_half(const Args& a, const uint16_t* Kl, const uint16_t* Vl, int ks0, int qw, int q,
-                                         const u32x4 (&qf)[HPW][D / 16], float (&m2)[HPW], float (&lsum)[HPW],
+                                         const u32x4 (&qf)[HPW][kQFrags<D, F8>], float (&m2)[HPW], float (&lsum)[HPW],
                                          f32x16 (&acc)[HPW][D >= 32 ? D / 32 : 1], const float* pat,
                                          EdgeOffsets eo) {
-  constexpr int KS = D / 16;
+  constexpr int KS = kQFrags<D, F8>;
   constexpr int DB = D >= 32 ? D / 32 : 1;
   const int lane = threadIdx.x & 63;
   const int r32 = lane & 31, hf = lane >> 5;
@@ -84,14 +90,28 @@ __device__ __forceinline__ void fwd_half(const Args& a, const uint16_t* Kl, cons
   // Head by head: head 0's scores are complete while head 1's MFMAs are still in the
   // pipe, and head 0's softmax (VALU) overlaps them.
   u32x4 kf[KS];
+  if constexpr (F8) {
+    // e4m3 K rows of D bytes, swizzled like 16-bit rows of D / 2 elements
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-    kf[ks] = *reinterpret_cast<const u32x4*>(Kl + swz_off<D>(r32, hf * (D / 2) + 8 * ks));
+    for (int f = 0; f < KS; ++f)
+      kf[f] = *reinterpret_cast<const u32x4*>(Kl + swz_off<D / 2>(r32, 8 * (4 * (f / 2) + 2 * hf + f % 2)));
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      kf[ks] = *reinterpret_cast<const u32x4*>(Kl + swz_off<D>(r32, hf * (D / 2) + 8 * ks));
+  }
   auto qk = [&](const f32x16& c0) {
 #pragma unroll
-    for (int h = 0; h < HPW; ++h)
+    for (int h = 0; h < HPW; ++h) {
+      if constexpr (F8) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) s[h] = E::mfma(kf[ks], qf[h][ks], ks == 0 ? c0 : s[h]);
+        for (int kb = 0; kb < KS / 2; ++kb)
+          s[h] = mfma_fp8(kf[2 * kb], kf[2 * kb + 1], qf[h][2 * kb], qf[h][2 * kb + 1], kb == 0 ? c0 : s[h]);
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) s[h] = E::mfma(kf[ks], qf[h][ks], ks == 0 ? c0 : s[h]);
+      }
+    }
   };
   if (tile_full(ks0, qw, W, S)) {
     qk(f32x16{});
@@ -166,19 +186,25 @@ __device__ __forceinline__ void fwd_half(const Args& a, const uint16_t* Kl, cons
   }
 }
 
-template <typename E, int D, int HPW>
+// F8: q, k, v hold OCP e4m3 values (fa_fwd_fp8); Q K^T runs on the fp8 MFMA, V is widened to
+// bf16 (exactly) on its way into LDS so that P V is the 16-bit path's, and O (type E = BF16) is
+// scaled by a.oscale, the dequantisation factor of V.
+template <typename E, int D, int HPW, bool F8>
 __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   constexpr int BN = 64;                   // keys per LDS block
-  constexpr int KS = D / 16;               // reduction steps over the head dim
+  constexpr int KS = kQFrags<D, F8>;       // 16-byte Q fragments per head and lane
   constexpr int DB = D >= 32 ? D / 32 : 1; // 32-row C tiles of O^T
-  constexpr int BUF = 2 * BN * D;          // K, then V, both swizzled row-major [key][d]
-  constexpr int CPB = BN * D / 8;          // 16-byte chunks per 64-key block of K (or V)
+  constexpr int EB = F8 ? 1 : 2;           // bytes per input element
+  constexpr int KBUF = BN * D * EB / 2;    // K block in LDS (16-bit units), swizzled row-major [key][d]
+  constexpr int BUF = KBUF + BN * D;       // K, then V as 16-bit values, swizzled row-major [key][d]
+  constexpr int CPR = D * EB / 16;         // 16-byte chunks per K (or V) row in memory
+  constexpr int CPB = BN * CPR;            // 16-byte chunks per 64-key block of K (or V)
   constexpr int NK = (CPB + 255) / 256;    // chunks per thread
   constexpr bool ALL_ON = CPB >= 256;      // every thread loads a chunk of every tile
   constexpr int NX = 8;                    // XCDs: workgroup i runs on XCD i % 8
-  // D = 128 reads Q straight into registers: a stash would take LDS that a second resident
-  // workgroup per CU needs.
-  constexpr bool kStash = D <= 64;
+  // 16-bit D = 128 reads Q straight into registers: a stash would take LDS that a second
+  // resident workgroup per CU needs.
+  constexpr bool kStash = F8 || D <= 64;
   constexpr int STASH = kStash ? HPW * KS * 512 : 0;  // per wave: the next tile's Q fragments
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF + 4 * STASH + 2 * kPatterns * kPatternFloats];
 
@@ -233,11 +259,14 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   uint16_t* stash = lds + 2 * BUF + wave * STASH;
   auto q_rsrc = [&](const TileIdx& t, int h) {
     KArgs& A = args_fresh();
-    return make_rsrc(reinterpret_cast<const char*>(A.q) + 2 * slice_off(A.sq, t.b, t.hw + h, t.row),
-                     span_bytes(t.L, A.sq[2], D));
+    return make_rsrc(reinterpret_cast<const char*>(A.q) + EB * slice_off(A.sq, t.b, t.hw + h, t.row),
+                     span_bytes(t.L, A.sq[2], D, EB));
   };
   auto q_off = [&](const TileIdx& t, int ks) {
-    return uint32_t((int64_t(t.qw + r32) * args_fresh().sq[2] + hf * (D / 2) + 8 * ks) * 2);
+    if constexpr (F8)
+      return uint32_t(int64_t(t.qw + r32) * args_fresh().sq[2] + 64 * (ks / 2) + 32 * hf + 16 * (ks % 2));
+    else
+      return uint32_t((int64_t(t.qw + r32) * args_fresh().sq[2] + hf * (D / 2) + 8 * ks) * 2);
   };
   auto stash_rows = [&](const TileIdx& t) {
 #pragma unroll
@@ -249,13 +278,17 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   };
 
   // K/V staging offsets of the thread's first chunk (the same for every tile); chunk it lies
-  // RSTEP rows further, which keeps the swizzle (it depends on the row mod 8 only).
-  constexpr int RSTEP = 256 / (D / 8);
-  const int row0 = tid / (D / 8), col0 = tid % (D / 8);
-  const uint32_t off_k0 = uint32_t((int64_t(row0) * a.sk[2] + 8 * col0) * 2);
-  const uint32_t off_v0 = uint32_t((int64_t(row0) * a.sv[2] + 8 * col0) * 2);
-  const int off_l0 = swz_off<D>(row0, 8 * col0);
-  const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
+  // RSTEP rows further, which keeps the swizzle (it depends on the row mod 8 only).  e4m3 K rows
+  // go to LDS as they are (swizzled like 16-bit rows of D / 2 elements); e4m3 V chunks become
+  // two 16-bit chunks of the 16-bit V tile.
+  constexpr int RSTEP = 256 / CPR;
+  const int row0 = tid / CPR, col0 = tid % CPR;
+  const uint32_t off_k0 = uint32_t(int64_t(row0) * a.sk[2] * EB + 16 * col0);
+  const uint32_t off_v0 = uint32_t(int64_t(row0) * a.sv[2] * EB + 16 * col0);
+  const int off_l0 = F8 ? swz_off<D / 2>(row0, 8 * col0) : swz_off<D>(row0, 8 * col0);
+  const int off_lv0 = F8 ? swz_off<D>(row0, 16 * col0) : off_l0;
+  const int off_lv1 = F8 ? swz_off<D>(row0, 16 * col0 + 8) : off_l0;
+  const uint32_t bk = uint32_t(EB * a.sk[2]), bv = uint32_t(EB * a.sv[2]);  // bytes per key row
 
   // the recurring masks (made visible by the barrier before the first key block)
   float* const pat = reinterpret_cast<float*>(lds + 2 * BUF + 4 * STASH);
@@ -306,10 +339,10 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // K/V of the KV head through buffer resources spanning the sequence's rows [0, L): rows past L
   // read as zero, so the loads need no branches (a slice is < 2^31 bytes, checked by the C ABI).
   KArgs& Akv = args_fresh();
-  const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(Akv.k) + 2 * slice_off(Akv.sk, b, kvh, t.row),
-                              span_bytes(L, Akv.sk[2], D));
-  const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(Akv.v) + 2 * slice_off(Akv.sv, b, kvh, t.row),
-                              span_bytes(L, Akv.sv[2], D));
+  const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(Akv.k) + EB * slice_off(Akv.sk, b, kvh, t.row),
+                              span_bytes(L, Akv.sk[2], D, EB));
+  const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(Akv.v) + EB * slice_off(Akv.sv, b, kvh, t.row),
+                              span_bytes(L, Akv.sv[2], D, EB));
 
   // Register staging of the next LDS block.
   u32x4 kreg[NK], vreg[NK];
@@ -324,12 +357,20 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   };
   auto sstore = [&](int buf) {
     uint16_t* Kl = lds + buf * BUF;
-    uint16_t* Vl = Kl + BN * D;
+    uint16_t* Vl = Kl + KBUF;
 #pragma unroll
     for (int it = 0; it < NK; ++it) {
       if (ALL_ON || tid + 256 * it < CPB) {
-        st16(Kl + off_l0 + RSTEP * D * it, kreg[it]);
-        st16(Vl + off_l0 + RSTEP * D * it, vreg[it]);
+        if constexpr (F8) {
+          st16(Kl + off_l0 + RSTEP * (D / 2) * it, kreg[it]);
+          u32x4 v0, v1;
+          fp8x16_to_bf16(vreg[it], v0, v1);
+          st16(Vl + off_lv0 + RSTEP * D * it, v0);
+          st16(Vl + off_lv1 + RSTEP * D * it, v1);
+        } else {
+          st16(Kl + off_l0 + RSTEP * D * it, kreg[it]);
+          st16(Vl + off_l0 + RSTEP * D * it, vreg[it]);
+        }
       }
     }
   };
@@ -351,12 +392,13 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     }
     if (wave_active) {
       const uint16_t* Kl = lds + (i & 1) * BUF;
-      const uint16_t* Vl = Kl + BN * D;
+      const uint16_t* Vl = Kl + KBUF;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
         const int ks0 = kb + 32 * sb;
         if (!wave_needs(ks0, qw, L, W, S)) continue;
-        fwd_half<E, D, HPW>(a, Kl + 32 * sb * D, Vl + 32 * sb * D, ks0, qw, q, qf, m2, lsum, acc, pat, eo);
+        fwd_half<E, D, HPW, F8>(a, Kl + 32 * sb * (KBUF / BN), Vl + 32 * sb * D, ks0, qw, q, qf, m2, lsum, acc, pat,
+                                eo);
       }
     }
     if (more) sstore((i + 1) & 1);
@@ -386,7 +428,8 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
       lt = lt * r + fast_exp2(sl - mn);
       mt = mn;
     }
-    const float inv = lt > 0.f ? r / lt : 0.f;
+    float inv = lt > 0.f ? r / lt : 0.f;
+    if constexpr (F8) inv *= A.oscale;
     char* op = reinterpret_cast<char*>(A.o_out) + 2 * slice_off(A.so_out, b, hw + h, t.row + q);
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
@@ -419,7 +462,7 @@ static int fwd_resident_per_cu() {
   return cached;
 }
 
-template <typename E, int D, int HPW>
+template <typename E, int D, int HPW, bool F8 = false>
 static hipError_t launch_fwd_h(const Args& a, hipStream_t stream) {
   const int n_tiles = a.n_qtiles * (a.B * a.Hq / (HPW * a.wh));
   int dev = 0, cus = 0;
@@ -427,9 +470,9 @@ static hipError_t launch_fwd_h(const Args& a, hipStream_t stream) {
       cus < 1)
     cus = 256;
   // one resident wave of workgroups, a multiple of the 8 XCDs
-  const int slots = fwd_resident_per_cu<fwd_kernel<E, D, HPW>>() * cus;
+  const int slots = fwd_resident_per_cu<fwd_kernel<E, D, HPW, F8>>() * cus;
   const int wgs = 8 * ((min(n_tiles, slots) + 7) / 8);
-  hipLaunchKernelGGL((fwd_kernel<E, D, HPW>), dim3(wgs), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((fwd_kernel<E, D, HPW, F8>), dim3(wgs), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -451,6 +494,14 @@ static hipError_t launch_fwd_e(const Args& a, int D, int hpw, hipStream_t stream
 
 hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stream) {
   return dtype == 1 ? launch_fwd_e<BF16>(a, D, hpw, stream) : launch_fwd_e<F16>(a, D, hpw, stream);
+}
+
+// e4m3 inputs, bf16 output: D = 64 shares K/V fragments between two heads per wave where the
+// group size allows, D = 128 has one head per wave.
+hipError_t launch_fwd_fp8(const Args& a, int D, int hpw, hipStream_t stream) {
+  if (D == 64) return hpw == 2 ? launch_fwd_h<BF16, 64, 2, true>(a, stream) : launch_fwd_h<BF16, 64, 1, true>(a, stream);
+  if (D == 128 && hpw == 1) return launch_fwd_h<BF16, 128, 1, true>(a, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace fa

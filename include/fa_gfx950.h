@@ -37,10 +37,11 @@
 extern "C" {
 #endif
 
-#define FA_GFX950_VERSION 10200 /* 1.2.0 */
+#define FA_GFX950_VERSION 10300 /* 1.3.0 */
 
-/* Element types of q/k/v/o/dout/dq/dk/dv.  All of them share one type per call. */
-enum fa_dtype { FA_DTYPE_BF16 = 1, FA_DTYPE_F16 = 2 };
+/* Element types of q/k/v/o/dout/dq/dk/dv.  All of them share one type per call, except in
+ * fa_fwd_fp8: FA_DTYPE_FP8_E4M3 means OCP float8 e4m3 q, k, v and a bf16 o. */
+enum fa_dtype { FA_DTYPE_BF16 = 1, FA_DTYPE_F16 = 2, FA_DTYPE_FP8_E4M3 = 3 };
 
 enum fa_status {
   FA_OK = 0,
@@ -48,8 +49,9 @@ enum fa_status {
   FA_ERR_SHAPE = -2,       /* B, Hq, Hkv or L < 1, or Hq % Hkv != 0 */
   FA_ERR_HEAD_DIM = -3,    /* D not in {16, 32, 64, 128} */
   FA_ERR_DTYPE = -4,       /* dtype not an fa_dtype */
-  FA_ERR_ALIGN = -5,       /* a 16-bit tensor's base not 16-byte aligned, or a stride negative or
-                              not a multiple of 8 elements; lse not 4-byte aligned */
+  FA_ERR_ALIGN = -5,       /* a tensor's base not 16-byte aligned, or a stride negative or not a
+                              multiple of 16 bytes (8 16-bit or 16 e4m3 elements); lse not 4-byte
+                              aligned */
   FA_ERR_MASK = -6,        /* window < 1 and sink < 1: every query row would be fully masked */
   FA_ERR_WORKSPACE = -7,   /* workspace NULL or smaller than fa_bwd_workspace_bytes() */
   FA_ERR_LAUNCH = -8,      /* a HIP launch failed */
@@ -172,6 +174,18 @@ int fa_fwd_varlen(const fa_fwd_params* p, const int32_t* cu_seqlens, int32_t tot
                   void* stream);
 int fa_bwd_varlen(const fa_bwd_params* p, const int32_t* cu_seqlens, int32_t total_rows, const float* sinks,
                   float* dsinks, void* workspace, size_t workspace_bytes, void* stream);
+
+/* FP8 forward: q, k and v hold OCP float8 e4m3 values (p->dtype = FA_DTYPE_FP8_E4M3, strides in
+ * elements, i.e. bytes, multiples of 16, bases 16-byte aligned); the values they stand for are
+ * q_descale * q, k_descale * k and v_descale * v.  o is written in bf16 (strides in bf16
+ * elements, multiples of 8) and lse as by fa_fwd.  head_dim is 64 or 128.  Q K^T runs on the fp8
+ * matrix cores; V is widened to bf16 exactly and P V runs as in fa_fwd, so the result is fa_fwd's
+ * bf16 result for the dequantised inputs.  sinks (float32 [Hq] learned logits) may be NULL.  The
+ * reference has no fp8 path (its kernels take fp16 / bf16 / fp32 tensors,
+ * flash_attention_gpt_oss.py:356-383); this is the forward for the compute-bound shapes (long
+ * full-causal layers, D = 128), forward only. */
+int fa_fwd_fp8(const fa_fwd_params* p, float q_descale, float k_descale, float v_descale, const float* sinks,
+               void* stream);
 
 /* Host-only argument checks used by fa_fwd / fa_bwd (no HIP call is made). */
 int fa_check_fwd(const fa_fwd_params* p);

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_strerror():
     L = _lib.lib()
-    assert L.fa_version() == 10200
+    assert L.fa_version() == 10300
     codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10]
     texts = [_lib.strerror(c) for c in codes]
     assert len(set(texts)) == len(codes)
@@ -245,3 +245,31 @@ def test_varlen_entry_points_reject_before_any_hip_call():
                            None) == _lib.FA_ERR_NULL
     assert L.fa_bwd_varlen(ctypes.byref(_bwd_params()), cu, 100, None, None, ctypes.c_void_p(256),
                            ctypes.c_size_t(0), None) == _lib.FA_ERR_WORKSPACE
+
+
+def test_fp8_entry_point_rejects_before_any_hip_call():
+    """fa_fwd_fp8's own checks: e4m3 dtype code, D in {64, 128}, 16-byte strides of the e4m3
+    tensors (8-element strides of the bf16 output), finite dequantisation factors."""
+    L = _lib.lib()
+    F8 = _lib.FA_DTYPE_FP8_E4M3
+
+    def call(p, qd=1.0, kd=1.0, vd=1.0, sinks=None):
+        return L.fa_fwd_fp8(ctypes.byref(p), qd, kd, vd, sinks, None)
+
+    assert L.fa_fwd_fp8(None, 1.0, 1.0, 1.0, None, None) == _lib.FA_ERR_NULL
+    assert call(_fwd_params(dtype=F8, v=None)) == _lib.FA_ERR_NULL
+    assert call(_fwd_params()) == _lib.FA_ERR_DTYPE  # bf16 code
+    assert call(_fwd_params(dtype=F8, head_dim=32)) == _lib.FA_ERR_HEAD_DIM
+    assert call(_fwd_params(dtype=F8, head_dim=16)) == _lib.FA_ERR_HEAD_DIM
+    assert call(_fwd_params(dtype=F8, head_dim=48)) == _lib.FA_ERR_HEAD_DIM
+    assert call(_fwd_params(dtype=F8), qd=float("nan")) == _lib.FA_ERR_SCALE
+    assert call(_fwd_params(dtype=F8), vd=float("inf")) == _lib.FA_ERR_SCALE
+    assert call(_fwd_params(dtype=F8, softmax_scale=1e30), qd=1e30) == _lib.FA_ERR_SCALE  # product overflows
+    assert call(_fwd_params(dtype=F8, window=0, sink=0)) == _lib.FA_ERR_MASK
+    # 72 is a valid 16-bit stride (a multiple of 8) but not 16 bytes of e4m3
+    assert call(_fwd_params(dtype=F8, q_stride=(8 * 128 * 72, 128 * 72, 72))) == _lib.FA_ERR_ALIGN
+    assert call(_fwd_params(dtype=F8, o_stride=(8 * 128 * 68, 128 * 68, 68))) == _lib.FA_ERR_ALIGN
+    assert call(_fwd_params(dtype=F8, k=(1 << 20) + 8)) == _lib.FA_ERR_ALIGN
+    assert call(_fwd_params(dtype=F8), sinks=ctypes.c_void_p(258)) == _lib.FA_ERR_ALIGN
+    # the 16-bit entry points do not take the e4m3 code
+    assert L.fa_check_fwd(ctypes.byref(_fwd_params(dtype=F8))) == _lib.FA_ERR_DTYPE
