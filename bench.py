@@ -264,6 +264,49 @@ def varlen_measure(steps, warmup, seqs=VARLEN_SEQS):
             "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s"}
 
 
+FP8_CONFIGS = ("c3", "c5", "c2")
+
+
+def fp8_forward_measure(iters=20, warmup=5, names=FP8_CONFIGS):
+    """Forward kernel time of the FP8 path (fa_fwd_fp8: e4m3 q, k, v quantised per tensor with
+    quantize_fp8, bf16 o) beside the 16-bit forward (fa_fwd) on the same configs, inputs resident
+    in HBM, HIP events around `iters` back-to-back launches.  Useful FLOPs are the forward's
+    (4 D pairs B Hq)."""
+    import torch
+
+    fa = _pkg()
+    ops = _mod("_ops")
+    flops_mod = _mod("flops")
+    dev = torch.device("cuda", 0)
+    out = {}
+    for name in names:
+        cfg = CONFIGS[name]
+        q, k, v, _ = make_inputs(cfg, dev)
+        sc = 1.0 / math.sqrt(cfg["D"])
+        (q8, qd), (k8, kd), (v8, vd) = (fa.quantize_fp8(t) for t in (q, k, v))
+        calls = {"16bit": ops.FwdCall(q, k, v, cfg["W"], cfg["S"], sc),
+                 "fp8": ops.Fp8FwdCall(q8, k8, v8, cfg["W"], cfg["S"], sc, (qd, kd, vd))}
+        us = {}
+        for tag, call in calls.items():
+            for _ in range(warmup):
+                call.run()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(iters):
+                call.run()
+            e1.record()
+            torch.cuda.synchronize()
+            us[tag] = e0.elapsed_time(e1) / iters * 1e3
+        wl = flops_mod.Workload(cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"], cfg["D"], cfg["W"], cfg["S"])
+        f = wl.flops("fwd")
+        out[name] = {"fwd_us_16bit": round(us["16bit"], 2), "fwd_us_fp8": round(us["fp8"], 2),
+                     "tflops_16bit": round(f / us["16bit"] / 1e6, 1), "tflops_fp8": round(f / us["fp8"] / 1e6, 1),
+                     "speedup": round(us["16bit"] / us["fp8"], 3), "dtype_16bit": cfg["dtype"]}
+        del q, k, v, q8, k8, v8, calls
+    return out
+
+
 def sdpa_baseline(cfg, q, k, v, do, steps=10, warmup=3):
     """PyTorch-ROCm SDPA with a boolean mask, the reference's second baseline
     (pytorch_sdpa_attention, benchmark_backward_speed.py:57-65), fwd + autograd bwd on the GPU in
@@ -376,6 +419,8 @@ def main():
     ap.add_argument("--cpu-baseline-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sdpa-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the packed-batch and fp8 entries of the c2 line (for per-kernel profiles of c2 alone)")
     ap.add_argument("--table", action="store_true", help="also time every BASELINE config (stderr)")
     ap.add_argument("--profile-launches", type=int, default=0, metavar="N",
                     help="only launch a 256 MiB copy and each kernel N times (for rocprofv3 --pmc runs)")
@@ -449,8 +494,9 @@ def main():
         "kernels": kernels,
         "roofline": roofline,
     }
-    if args.config == "c2":
+    if args.config == "c2" and not args.no_extras:
         line["varlen"] = varlen_measure(args.steps, args.warmup)
+        line["fp8_forward"] = fp8_forward_measure()
     if not args.no_sdpa_baseline:
         line["sdpa_baseline"] = sdpa_baseline(cfg, q, k, v, do)
     if not args.no_cpu_baseline:
