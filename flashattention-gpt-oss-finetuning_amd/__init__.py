@@ -17,6 +17,7 @@ FP8 (OCP e4m3) forward for the compute-bound shapes, D in {64, 128}, o in bfloat
 GPT-OSS integration (gpt_oss.py): learned per-head sink logits, [B, L, H, D] tensors, full and
 sliding layers, and transformers' attention-function interface:
     attention(q, k, v, window_size=None, sink_size=0, sinks=None, scale=None, layout="bhld")
+    padded_attention(q, k, v, attention_mask, window_size=None, sinks=None, scale=None)  # [B, L] mask
     FlashSWDAWithLearnedSinks.apply(q, k, v, sinks, window_size, sink_size=0, softmax_scale=None)
     register_transformers("fa_gfx950")   # attn_implementation="fa_gfx950"
 
@@ -26,7 +27,7 @@ The directory name is not a Python identifier; import it with
 from .attention import (FlashSWDAWithLearnedSinks, FlashSWDAWithSink, FlashSWDAWithSinkVarlen,  # noqa: F401
                         flash_swda_with_sink, flash_swda_with_sink_fp8, flash_swda_with_sink_varlen,
                         quantize_fp8, swa_sink_attention)
-from .gpt_oss import attention, gpt_oss_attention_forward, register_transformers  # noqa: F401
+from .gpt_oss import attention, gpt_oss_attention_forward, padded_attention, register_transformers  # noqa: F401
 from .flops import Workload, allowed_pairs_per_head  # noqa: F401
 
 __all__ = [
@@ -40,6 +41,7 @@ __all__ = [
     "quantize_fp8",
     "attention",
     "gpt_oss_attention_forward",
+    "padded_attention",
     "register_transformers",
     "Workload",
     "allowed_pairs_per_head",

@@ -20,7 +20,7 @@ from typing import Optional
 
 import torch
 
-from .attention import FlashSWDAWithLearnedSinks, FlashSWDAWithSink
+from .attention import FlashSWDAWithLearnedSinks, FlashSWDAWithSink, flash_swda_with_sink_varlen
 
 
 def attention(q, k, v, window_size: Optional[int] = None, sink_size: int = 0, sinks: Optional[torch.Tensor] = None,
@@ -46,18 +46,53 @@ def gpt_oss_attention_forward(module, query, key, value, attention_mask, dropout
     (query/key/value [B, H, L, D], s_aux = the module's sinks, sliding_window None for full
     layers).  Returns (attn_output [B, L, H, D], None), as the eager function does.
 
-    Supported: training and prefill without padding (attention_mask None, or a 2-D mask of all
-    ones), no dropout.  Padded batches, KV caches (query shorter than key) and dropout raise
-    NotImplementedError rather than computing something else."""
+    Supported: training and prefill, no dropout.  attention_mask is None or the 2-D [B, L] padding
+    mask that transformers' flash-attention mask function hands over (True or 1 = a token); a
+    padded batch runs as a packed variable-length batch (padded_attention).  KV caches (query
+    shorter than key), other mask forms and dropout raise NotImplementedError rather than
+    computing something else."""
     if dropout:
         raise NotImplementedError("attention dropout is not implemented by the gfx950 kernels")
     if query.shape[2] != key.shape[2]:
         raise NotImplementedError("query and key lengths differ (KV cache decoding); only full sequences are supported")
     if attention_mask is not None:
-        if attention_mask.dim() != 2 or not bool(attention_mask.all()):
-            raise NotImplementedError("padded batches are not supported; pass unpadded sequences (attention_mask None)")
+        if attention_mask.dim() != 2:
+            raise NotImplementedError("only the 2-D [batch, seq] padding mask of the flash-attention mask function "
+                                      f"is supported, got a {attention_mask.dim()}-D mask")
+        if not bool(attention_mask.all()):
+            o = padded_attention(query, key, value, attention_mask, window_size=sliding_window, sinks=s_aux,
+                                 scale=scaling)
+            return o, None
     o = attention(query, key, value, window_size=sliding_window, sinks=s_aux, scale=scaling)
     return o.transpose(1, 2), None
+
+
+def padded_attention(q, k, v, attention_mask, window_size: Optional[int] = None, sinks: Optional[torch.Tensor] = None,
+                     scale: Optional[float] = None):
+    """Attention over a padded batch: q [B, Hq, L, D], k/v [B, Hkv, L, D], attention_mask [B, L]
+    (nonzero = token).  The tokens of each row are gathered, in order, into one packed batch with
+    cu_seqlens and run through flash_swda_with_sink_varlen, so causality, the window and the sinks
+    count positions from each sequence's first token (left and right padding alike; a row with
+    gaps is concatenated, as flash-attention's unpadding does).  Returns o [B, L, Hq, D] with
+    zeros at padded positions; gradients flow through the gather and scatter."""
+    B, Hq, L, D = q.shape
+    if tuple(attention_mask.shape) != (B, L):
+        raise ValueError(f"attention_mask must be [B, L] = [{B}, {L}], got {tuple(attention_mask.shape)}")
+    m = attention_mask.to(device=q.device, dtype=torch.bool)
+    idx = m.reshape(-1).nonzero().squeeze(1)  # token rows of the [B * L] flattening, in order
+    lens = m.sum(1, dtype=torch.int32)
+    cu = torch.zeros(B + 1, dtype=torch.int32, device=q.device)
+    cu[1:] = lens.cumsum(0)
+    max_len = int(lens.max()) if B else 0
+    if max_len == 0:
+        return q.new_zeros(B, L, Hq, D)
+
+    def pack(x):  # [B, H, L, D] -> [tokens, H, D]
+        return x.transpose(1, 2).reshape(B * L, x.shape[1], D).index_select(0, idx)
+
+    W = max_len if window_size is None else int(window_size)
+    op = flash_swda_with_sink_varlen(pack(q), pack(k), pack(v), cu, max_len, W, 0, scale, sinks)
+    return op.new_zeros(B * L, Hq, D).index_copy(0, idx, op).view(B, L, Hq, D)
 
 
 def register_transformers(name: str = "fa_gfx950") -> str:

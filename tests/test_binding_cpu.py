@@ -48,7 +48,10 @@ def test_gpt_oss_adapter_host_checks(fa):
         fa.gpt_oss_attention_forward(None, q, k, k, None, dropout=0.1)
     with pytest.raises(NotImplementedError, match="KV cache"):
         fa.gpt_oss_attention_forward(None, q[:, :, :4], k, k, None)
-    with pytest.raises(NotImplementedError, match="padded"):
+    with pytest.raises(NotImplementedError, match="2-D"):
+        fa.gpt_oss_attention_forward(None, q, k, k, torch.ones(1, 1, 8, 8, dtype=torch.bool))
+    # a padded batch takes the packed path, which has no CPU implementation
+    with pytest.raises(RuntimeError, match="no CPU implementation"):
         fa.gpt_oss_attention_forward(None, q, k, k, torch.tensor([[1, 1, 1, 1, 1, 1, 1, 0]]))
     # CPU tensors reach the library boundary and fail loudly: there is no CPU implementation
     with pytest.raises(RuntimeError, match="no CPU implementation"):

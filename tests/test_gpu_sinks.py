@@ -219,3 +219,67 @@ def test_transformers_gpt_oss_attention_module(gpu, fa, layer_idx):
     assert rel(ours.sinks.grad, ref.sinks.grad) < 3e-2
     assert rel(ours.q_proj.weight.grad, ref.q_proj.weight.grad) < 2e-2
     assert rel(ours.k_proj.weight.grad, ref.k_proj.weight.grad) < 2e-2
+
+
+@pytest.mark.parametrize("layer_idx", [0, 1], ids=["sliding", "full"])
+def test_transformers_gpt_oss_attention_padded_batch(gpu, fa, layer_idx):
+    """A padded batch -- row 0 right-padded, row 1 left-padded -- through the registered attention
+    function, with the 2-D padding mask the flash-attention mask function hands over, equals
+    transformers' eager GptOssAttention run on each sequence alone (float32, positions from 0):
+    outputs and input gradients on the tokens, and the parameter gradients of the attention path.
+    Padded positions come back as zeros and receive no gradient."""
+    mod = pytest.importorskip("transformers.models.gpt_oss.modeling_gpt_oss")
+    from transformers import GptOssConfig
+
+    name = fa.register_transformers("fa_gfx950")
+    cfg = dict(hidden_size=256, num_attention_heads=8, num_key_value_heads=2, head_dim=64, sliding_window=24,
+               num_hidden_layers=2, layer_types=["sliding_attention", "full_attention"], attention_bias=True,
+               vocab_size=128, intermediate_size=64, num_local_experts=4)
+    ref_cfg, our_cfg = GptOssConfig(**cfg), GptOssConfig(**cfg)
+    ref_cfg._attn_implementation = "eager"
+    our_cfg._attn_implementation = name
+    torch.manual_seed(1)
+    ref = mod.GptOssAttention(ref_cfg, layer_idx).cuda()
+    with torch.no_grad():
+        for p in ref.parameters():
+            p.copy_((0.05 * torch.randn_like(p)).to(BF).float())
+        ref.sinks.copy_(torch.randn(8).to(BF).float())
+    ours = mod.GptOssAttention(our_cfg, layer_idx).cuda()
+    ours.load_state_dict(ref.state_dict())
+    ours = ours.to(BF)
+    rope = mod.GptOssRotaryEmbedding(ref_cfg).cuda()
+    B, L = 2, 80
+    mask = torch.zeros(B, L, dtype=torch.bool, device="cuda")
+    mask[0, :60] = True   # right padding
+    mask[1, 13:] = True   # left padding
+    x = torch.randn(B, L, 256, device="cuda").to(BF)
+    g = torch.randn(B, L, 256, device="cuda")
+    g[~mask] = 0
+    pos = (mask.long().cumsum(-1) - 1).clamp(min=0)
+
+    xo = x.clone().requires_grad_()
+    yo, _ = ours(xo, rope(xo, pos), mask)
+    yo.backward(g.to(BF))
+
+    yr = torch.zeros(B, L, 256, device="cuda")
+    xr_grad = torch.zeros(B, L, 256, device="cuda")
+    for b in range(B):
+        sel = mask[b]
+        n = int(sel.sum())
+        xb = x[b:b + 1, sel].float().requires_grad_()
+        pb = torch.arange(n, device="cuda").unsqueeze(0)
+        W = ref.sliding_window if ref.sliding_window is not None else n
+        add = torch.zeros(n, n, device="cuda").masked_fill(~naive.allowed_mask(n, W, 0, device="cuda"), float("-inf"))
+        yb, _ = ref(xb, rope(xb, pb), add.view(1, 1, n, n))
+        yb.backward(g[b:b + 1, sel])
+        yr[b, sel] = yb.detach()[0]
+        xr_grad[b, sel] = xb.grad[0]
+
+    rel = lambda a, b: float((a.detach().float() - b.detach().float()).norm() / b.detach().float().norm())
+    assert rel(yo[mask], yr[mask]) < 1e-2
+    assert rel(xo.grad[mask], xr_grad[mask]) < 2e-2
+    assert float(xo.grad[~mask].abs().max()) == 0.0
+    assert rel(ours.sinks.grad, ref.sinks.grad) < 3e-2
+    assert rel(ours.q_proj.weight.grad, ref.q_proj.weight.grad) < 2e-2
+    assert rel(ours.k_proj.weight.grad, ref.k_proj.weight.grad) < 2e-2
+    assert rel(ours.v_proj.weight.grad, ref.v_proj.weight.grad) < 2e-2
