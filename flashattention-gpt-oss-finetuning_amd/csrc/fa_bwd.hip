@@ -450,8 +450,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
 // workgroups; every workgroup of such a block writes the fp32 partial sums of its sink rows to
 // its own slot of the workspace, and bwd_sink_fold_kernel adds the slots in a fixed order.
 // ---------------------------------------------------------------------------------------------
+// Adds up the sink keys' dK/dV partials (defined with bwd_sink_fold_kernel below).
 template <typename E, int D>
-__global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
+__device__ void fold_sink_keys(int b, int kvh, int nk, const Seq& sq);
+
+// D = 16 keeps four waves per SIMD (at most 128 VGPRs); the wider head dims need more registers.
+template <typename E, int D>
+__global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Args a) {
   constexpr int KS = D / 16;
   constexpr int DB = D >= 32 ? D / 32 : 1;
   constexpr int TILE = 32 * D;               // 32 rows of Q or dO, swizzled row-major
@@ -790,34 +795,42 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const Args a) {
       }
     }
   }
+
+  // dq_sink_mode with at most 256 (sink key, column) pairs: key block 0's workgroup folds its
+  // sink keys (see fold_sink_keys), one pair per thread; the barrier makes its own slot writes
+  // visible to all its threads.
+  if (a.sink_dq && partial_block && !is_chunk && min(S, kKvKeys) * D <= 256) {
+    __syncthreads();
+    fold_sink_keys<E, D>(b, kvh, min(min(S, kKvKeys), L), sq);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
 // Sink fold: the dK/dV rows of the split sink keys are the sum of fp32 partials: those the
 // dK/dV kernel's regular and chunk workgroups wrote for them and, in dq_sink_mode, those the dQ
-// kernel flushed (the flagged tiles of the (batch, KV head)).  A separate launch, so every
-// partial is visible without a device-wide fence inside the producing kernels.
-// One workgroup per (b, KV head, sink key): thread (g, d) adds slots g, g + NG, g + 2 NG, ...
-// (their loads in flight together), then the NG group sums are added in order g = 0, 1, ... --
-// a fixed order, so results are deterministic.
+// kernel flushed (the flagged tiles of the (batch, KV head)).
+// fold_sink_key adds them for one sink key with the 256 threads of a workgroup: thread (g, d)
+// adds slots g, g + NG, g + 2 NG, ... (their loads in flight together), then the NG group sums
+// are added in order g = 0, 1, ... -- a fixed order, so results are deterministic.
+// bwd_sink_fold_kernel runs it in a launch of its own after the dK/dV kernel (every partial is
+// then visible without a device-wide fence).  In dq_sink_mode the dQ kernel's slots are complete
+// before the dK/dV kernel starts and the only other partial is that of key block 0's own
+// workgroup, so when the sink keys' (key, column) pairs fit one pass of 256 threads that
+// workgroup folds them itself after writing its slot (fold_sink_keys, one pair per thread, the
+// slots in the same order) and no fold launch follows.
 // ---------------------------------------------------------------------------------------------
 template <typename E, int D>
-__global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
+__device__ void fold_sink_key(int b, int kvh, int key, const Seq& sq, float (&part)[2][256 / D][D]) {
+  KArgs& Ak = args_fresh();
   constexpr int NG = 256 / D;  // slot groups
   constexpr int kBatch = 16;
-  __shared__ float part[2][NG][D];
-  const int nrows = min(a.S, kKvKeys * a.nsp);  // sink keys of the chunked blocks
-  const int key = blockIdx.x % nrows;
-  const int bh = blockIdx.x / nrows;  // b * Hkv + kvh
-  const int kvh = bh % a.Hkv, b = bh / a.Hkv;
-  const Seq sq = seq_of(a, b);
-  if (key >= sq.L) return;  // a sink key past the end of a short sequence: no such row
+  const int bh = b * Ak.Hkv + kvh;
   const int kblk = key / kKvKeys, row = key % kKvKeys;
   const int d = threadIdx.x % D, g = threadIdx.x / D;
-  const int64_t blk = int64_t(bh) * a.nsp + kblk;
-  const int64_t slot_stride = int64_t(2) * a.srows * D;
-  const float* src = a.partial + blk * (a.n_chunks + 1) * slot_stride + row * D + d;
-  const int ns = a.n_chunks + 1;
+  const int64_t blk = int64_t(bh) * Ak.nsp + kblk;
+  const int64_t slot_stride = int64_t(2) * Ak.srows * D;
+  const float* src = Ak.partial + blk * (Ak.n_chunks + 1) * slot_stride + row * D + d;
+  const int ns = Ak.n_chunks + 1;
   float sk = 0.f, sv = 0.f;
   for (int s0 = g; s0 < ns; s0 += NG * kBatch) {
     float xk[kBatch], xv[kBatch];
@@ -827,7 +840,7 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
       const bool in = sl < ns;
       const float* p = src + int64_t(in ? sl : 0) * slot_stride;
       xk[j] = in ? p[0] : 0.f;
-      xv[j] = in ? p[a.srows * D] : 0.f;
+      xv[j] = in ? p[Ak.srows * D] : 0.f;
     }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
@@ -835,19 +848,19 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
       sv += xv[j];
     }
   }
-  if (a.sink_dq) {
+  if (Ak.sink_dq) {
     // The dQ kernel's flushed partials of this (b, KV head) = tiles [(b + B kvh) tpk, + tpk): on
-    // XCD x, whose tiles are [x_lo, x_hi) and whose a.dq_wgs / 8 workgroups stride through them,
-    // the runs start at the first a.dq_wgs / 8 tiles of [max(x_lo, lo), min(x_hi, hi)).  All the
+    // XCD x, whose tiles are [x_lo, x_hi) and whose Ak.dq_wgs / 8 workgroups stride through them,
+    // the runs start at the first Ak.dq_wgs / 8 tiles of [max(x_lo, lo), min(x_hi, hi)).  All the
     // loads are independent; slots are added in (XCD, tile) order.
     constexpr int nx = 8;
-    const int tpk = a.n_qtiles * (a.G / a.wh);
-    const int n_tiles = tpk * a.B * a.Hkv;
-    const int wgs_x = a.dq_wgs / nx;
-    const int lo = (b + a.B * kvh) * tpk, hi = lo + tpk;
+    const int tpk = Ak.n_qtiles * (Ak.G / Ak.wh);
+    const int n_tiles = tpk * Ak.B * Ak.Hkv;
+    const int wgs_x = Ak.dq_wgs / nx;
+    const int lo = (b + Ak.B * kvh) * tpk, hi = lo + tpk;
     const int per = n_tiles / nx, rem = n_tiles % nx;
-    const int n_out = 2 * a.srows * D;
-    const float* dsrc = a.dq_sink_part + row * D + d;
+    const int n_out = 2 * Ak.srows * D;
+    const float* dsrc = Ak.dq_sink_part + row * D + d;
     for (int x = 0; x < nx; ++x) {
       const int x_lo = x * per + min(x, rem), x_hi = x_lo + per + (x < rem ? 1 : 0);
       const int A = max(x_lo, lo), B = min(x_hi, hi);
@@ -859,7 +872,7 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
           const int jj = j0 + j * NG;
           const float* p = dsrc + int64_t(A + (jj < n ? jj : 0)) * n_out;
           xk[j] = jj < n ? p[0] : 0.f;
-          xv[j] = jj < n ? p[a.srows * D] : 0.f;
+          xv[j] = jj < n ? p[Ak.srows * D] : 0.f;
         }
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
@@ -872,16 +885,74 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
   part[0][g][d] = sk;
   part[1][g][d] = sv;
   __syncthreads();
-  if (g != 0) return;
-  float tk = 0.f, tv = 0.f;
+  if (g == 0) {
+    float tk = 0.f, tv = 0.f;
 #pragma unroll
-  for (int j = 0; j < NG; ++j) {
-    tk += part[0][j][d];
-    tv += part[1][j][d];
+    for (int j = 0; j < NG; ++j) {
+      tk += part[0][j][d];
+      tv += part[1][j][d];
+    }
+    const uint32_t pk = E::pack2(tk * Ak.scale, tv);
+    reinterpret_cast<uint16_t*>(Ak.dk)[slice_off(Ak.sdk, b, kvh, sq.row + key) + d] = uint16_t(pk);
+    reinterpret_cast<uint16_t*>(Ak.dv)[slice_off(Ak.sdv, b, kvh, sq.row + key) + d] = uint16_t(pk >> 16);
   }
-  const uint32_t pk = E::pack2(tk * a.scale, tv);
-  reinterpret_cast<uint16_t*>(a.dk)[slice_off(a.sdk, b, kvh, sq.row + key) + d] = uint16_t(pk);
-  reinterpret_cast<uint16_t*>(a.dv)[slice_off(a.sdv, b, kvh, sq.row + key) + d] = uint16_t(pk >> 16);
+  __syncthreads();  // part is free again
+}
+
+template <typename E, int D>
+__device__ void fold_sink_keys(int b, int kvh, int nk, const Seq& sq) {
+  KArgs& Ak = args_fresh();
+  constexpr int kBatch = 16;
+  const int t = threadIdx.x, key = t / D, d = t % D;
+  if (key >= nk) return;
+  const int64_t slot_stride = int64_t(2) * Ak.srows * D;
+  const int64_t blk = int64_t(b * Ak.Hkv + kvh) * Ak.nsp;  // key block 0
+  const float* own = Ak.partial + blk * (Ak.n_chunks + 1) * slot_stride + key * D + d;
+  float sk = own[0], sv = own[Ak.srows * D];
+  // the dQ kernel's runs of this (b, KV head), in (XCD, tile) order as in fold_sink_key
+  constexpr int nx = 8;
+  const int tpk = Ak.n_qtiles * (Ak.G / Ak.wh);
+  const int n_tiles = tpk * Ak.B * Ak.Hkv;
+  const int wgs_x = Ak.dq_wgs / nx;
+  const int lo = (b + Ak.B * kvh) * tpk, hi = lo + tpk;
+  const int per = n_tiles / nx, rem = n_tiles % nx;
+  const int n_out = 2 * Ak.srows * D;
+  const float* dsrc = Ak.dq_sink_part + key * D + d;
+  for (int x = 0; x < nx; ++x) {
+    const int x_lo = x * per + min(x, rem), x_hi = x_lo + per + (x < rem ? 1 : 0);
+    const int r_lo = max(x_lo, lo), r_hi = min(x_hi, hi);
+    const int n = r_hi > r_lo ? min(wgs_x, r_hi - r_lo) : 0;
+    for (int j0 = 0; j0 < n; j0 += kBatch) {
+      float xk[kBatch], xv[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int jj = j0 + j;
+        const float* p = dsrc + int64_t(r_lo + (jj < n ? jj : 0)) * n_out;
+        xk[j] = jj < n ? p[0] : 0.f;
+        xv[j] = jj < n ? p[Ak.srows * D] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        sk += xk[j];
+        sv += xv[j];
+      }
+    }
+  }
+  const uint32_t pk = E::pack2(sk * Ak.scale, sv);
+  reinterpret_cast<uint16_t*>(Ak.dk)[slice_off(Ak.sdk, b, kvh, sq.row + key) + d] = uint16_t(pk);
+  reinterpret_cast<uint16_t*>(Ak.dv)[slice_off(Ak.sdv, b, kvh, sq.row + key) + d] = uint16_t(pk >> 16);
+}
+
+template <typename E, int D>
+__global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
+  __shared__ float part[2][256 / D][D];
+  const int nrows = min(a.S, kKvKeys * a.nsp);  // sink keys of the chunked blocks
+  const int key = blockIdx.x % nrows;
+  const int bh = blockIdx.x / nrows;  // b * Hkv + kvh
+  const int kvh = bh % a.Hkv, b = bh / a.Hkv;
+  const Seq sq = seq_of(a, b);
+  if (key >= sq.L) return;  // a sink key past the end of a short sequence: no such row
+  fold_sink_key<E, D>(b, kvh, key, sq, part);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -952,13 +1023,14 @@ static hipError_t launch_dq_d(const Args& a, int, hipStream_t stream) {
 template <typename E, int D>
 static hipError_t launch_dkdv_d(const Args& a, hipStream_t stream) {
   const dim3 grid(a.n_chunk_wgs + a.B * a.Hkv * a.n_kblocks), block(256);
-  hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), grid, block, 0, stream, a);
+  Args ad = a;
+  if (a.sink_dq) ad.dq_wgs = dq_grid<E, D, true>(a);  // the in-kernel fold finds the dQ slots by it
+  hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), grid, block, 0, stream, ad);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || a.nsp == 0) return e;
+  // dq_sink_mode with at most 256 (sink key, column) pairs folds inside the dK/dV kernel
+  if (e != hipSuccess || a.nsp == 0 || (a.sink_dq && min(a.S, kKvKeys) * D <= 256)) return e;
   const int64_t n = int64_t(a.B) * a.Hkv * min(a.S, kKvKeys * a.nsp);  // one workgroup per sink key
-  Args af = a;
-  if (a.sink_dq) af.dq_wgs = dq_grid<E, D, true>(a);
-  hipLaunchKernelGGL((bwd_sink_fold_kernel<E, D>), dim3(unsigned(n)), block, 0, stream, af);
+  hipLaunchKernelGGL((bwd_sink_fold_kernel<E, D>), dim3(unsigned(n)), block, 0, stream, ad);
   return hipGetLastError();
 }
 
