@@ -10,15 +10,19 @@
 //
 // Launches:
 //  1. bwd_dq_kernel (query-major, same tiling as the forward): computes delta for its rows
-//     (stored in the workspace) and dQ over the sink + window key blocks.
+//     (stored in the workspace) and dQ over the sink + window key blocks.  With at most 16 sink
+//     keys in key block 0 (dq_sink_mode) it also accumulates those keys' dK/dV for the rows past
+//     block 0's window, flushing fp32 partials to the workspace.
 //  2. bwd_dkdv_kernel (key-major): a workgroup owns 64 keys of one KV head and sweeps the
 //     (query head, 32-row query block) pairs that can see those keys, bounded by the window:
 //     rows [k0, k0 + 63 + W).  Every sum is formed in a fixed order, so results are
-//     deterministic.  Sink keys are also seen by every later row; those rows are split into
-//     chunks of `chunk_rows` handled by extra workgroups of the same kernel (the reference
-//     instead loops one program over all of L for a sink block,
-//     benchmark_backward_speed.py:432-438).
-//  3. bwd_sink_fold_kernel (only when rows were chunked): adds the sink rows' partial sums.
+//     deterministic.  Sink keys are also seen by every later row; outside dq_sink_mode those
+//     rows are split into chunks of `chunk_rows` handled by extra workgroups of the same kernel
+//     (the reference instead loops one program over all of L for a sink block,
+//     benchmark_backward_speed.py:432-438).  In dq_sink_mode key block 0's workgroup adds the
+//     dQ kernel's partials to its own when its sink keys' columns fit one pass of 256 threads.
+//  3. bwd_sink_fold_kernel (when rows were chunked, or the in-kernel fold does not apply): adds
+//     the sink rows' partial sums.
 //  4. bwd_sink_logit_kernel (only with learned sink logits): adds the dQ kernel's per-row-block
 //     partials of the sink logits' gradient.
 #include <type_traits>
