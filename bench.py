@@ -268,10 +268,10 @@ FP8_CONFIGS = ("c3", "c5", "c2")
 
 
 def fp8_forward_measure(iters=20, warmup=5, names=FP8_CONFIGS):
-    """Forward kernel time of the FP8 path (fa_fwd_fp8: e4m3 q, k, v quantised per tensor with
-    quantize_fp8, bf16 o) beside the 16-bit forward (fa_fwd) on the same configs, inputs resident
-    in HBM, HIP events around `iters` back-to-back launches.  Useful FLOPs are the forward's
-    (4 D pairs B Hq)."""
+    """Forward kernel time of the FP8 paths (e4m3 q, k, v quantised per tensor with quantize_fp8,
+    bf16 o; fa_fwd_fp8: Q K^T in fp8, fa_fwd_fp8_pv: P V in fp8 as well) beside the 16-bit forward
+    (fa_fwd) on the same configs, inputs resident in HBM, HIP events around `iters` back-to-back
+    launches.  Useful FLOPs are the forward's (4 D pairs B Hq)."""
     import torch
 
     fa = _pkg()
@@ -285,7 +285,8 @@ def fp8_forward_measure(iters=20, warmup=5, names=FP8_CONFIGS):
         sc = 1.0 / math.sqrt(cfg["D"])
         (q8, qd), (k8, kd), (v8, vd) = (fa.quantize_fp8(t) for t in (q, k, v))
         calls = {"16bit": ops.FwdCall(q, k, v, cfg["W"], cfg["S"], sc),
-                 "fp8": ops.Fp8FwdCall(q8, k8, v8, cfg["W"], cfg["S"], sc, (qd, kd, vd))}
+                 "fp8": ops.Fp8FwdCall(q8, k8, v8, cfg["W"], cfg["S"], sc, (qd, kd, vd)),
+                 "fp8_pv": ops.Fp8FwdCall(q8, k8, v8, cfg["W"], cfg["S"], sc, (qd, kd, vd), fp8_pv=True)}
         us = {}
         for tag, call in calls.items():
             for _ in range(warmup):
@@ -301,8 +302,11 @@ def fp8_forward_measure(iters=20, warmup=5, names=FP8_CONFIGS):
         wl = flops_mod.Workload(cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"], cfg["D"], cfg["W"], cfg["S"])
         f = wl.flops("fwd")
         out[name] = {"fwd_us_16bit": round(us["16bit"], 2), "fwd_us_fp8": round(us["fp8"], 2),
+                     "fwd_us_fp8_pv": round(us["fp8_pv"], 2),
                      "tflops_16bit": round(f / us["16bit"] / 1e6, 1), "tflops_fp8": round(f / us["fp8"] / 1e6, 1),
-                     "speedup": round(us["16bit"] / us["fp8"], 3), "dtype_16bit": cfg["dtype"]}
+                     "tflops_fp8_pv": round(f / us["fp8_pv"] / 1e6, 1),
+                     "speedup": round(us["16bit"] / us["fp8"], 3), "speedup_pv": round(us["16bit"] / us["fp8_pv"], 3),
+                     "dtype_16bit": cfg["dtype"]}
         del q, k, v, q8, k8, v8, calls
     return out
 

@@ -42,6 +42,7 @@ EXPORTS = (
     "fa_fwd_varlen",
     "fa_bwd_varlen",
     "fa_fwd_fp8",
+    "fa_fwd_fp8_pv",
     "fa_bwd_workspace_bytes",
     "fa_check_fwd",
     "fa_check_bwd",
@@ -141,9 +142,10 @@ def lib() -> ctypes.CDLL:
             L.fa_bwd_varlen.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p,
                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
             L.fa_bwd_varlen.restype = ctypes.c_int
-            L.fa_fwd_fp8.argtypes = [ctypes.POINTER(FwdParams), ctypes.c_float, ctypes.c_float, ctypes.c_float,
-                                     ctypes.c_void_p, ctypes.c_void_p]
-            L.fa_fwd_fp8.restype = ctypes.c_int
+            for fn in (L.fa_fwd_fp8, L.fa_fwd_fp8_pv):
+                fn.argtypes = [ctypes.POINTER(FwdParams), ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                               ctypes.c_void_p, ctypes.c_void_p]
+                fn.restype = ctypes.c_int
             L.fa_bwd_workspace_bytes.argtypes = [ctypes.c_int32] * 7
             L.fa_bwd_workspace_bytes.restype = ctypes.c_size_t
             L.fa_check_fwd.argtypes = [ctypes.POINTER(FwdParams)]

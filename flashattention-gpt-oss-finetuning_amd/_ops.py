@@ -178,12 +178,14 @@ def _fp8_ready(t: torch.Tensor) -> torch.Tensor:
 
 
 class Fp8FwdCall:
-    """A prepared fa_fwd_fp8 launch: q [B,Hq,L,D], k/v [B,Hkv,L,D] in torch.float8_e4m3fn standing
-    for descale[i] times their values; o is bfloat16 with q's memory layout, lse float32 [B,Hq,L]."""
+    """A prepared fa_fwd_fp8 launch (fa_fwd_fp8_pv with ``fp8_pv``: P V on the fp8 matrix cores too):
+    q [B,Hq,L,D], k/v [B,Hkv,L,D] in torch.float8_e4m3fn standing for descale[i] times their
+    values; o is bfloat16 with q's memory layout, lse float32 [B,Hq,L]."""
 
-    __slots__ = ("params", "inputs", "o", "lse", "device", "sinks", "descale")
+    __slots__ = ("params", "inputs", "o", "lse", "device", "sinks", "descale", "entry")
 
-    def __init__(self, q, k, v, window: int, sink: int, scale: float, descale=(1.0, 1.0, 1.0), sinks=None):
+    def __init__(self, q, k, v, window: int, sink: int, scale: float, descale=(1.0, 1.0, 1.0), sinks=None,
+                 fp8_pv: bool = False):
         dev = q.device
         if dev.type != "cuda":
             raise RuntimeError(f"q is on {dev}: the gfx950 attention kernels need GPU tensors "
@@ -216,22 +218,24 @@ class Fp8FwdCall:
         p.softmax_scale = scale
         p.dtype = _lib.FA_DTYPE_FP8_E4M3
         self.params = p
+        self.entry = "fa_fwd_fp8_pv" if fp8_pv else "fa_fwd_fp8"
 
     def run(self) -> None:
         qd, kd, vd = self.descale
         with _DeviceGuard(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
-            rc = _lib.lib().fa_fwd_fp8(ctypes.byref(self.params), ctypes.c_float(qd), ctypes.c_float(kd),
-                                       ctypes.c_float(vd),
-                                       ctypes.c_void_p(None if self.sinks is None else self.sinks.data_ptr()),
-                                       ctypes.c_void_p(stream))
-        _lib.raise_for_status(rc, "fa_fwd_fp8")
+            rc = getattr(_lib.lib(), self.entry)(ctypes.byref(self.params), ctypes.c_float(qd), ctypes.c_float(kd),
+                                                 ctypes.c_float(vd),
+                                                 ctypes.c_void_p(None if self.sinks is None else self.sinks.data_ptr()),
+                                                 ctypes.c_void_p(stream))
+        _lib.raise_for_status(rc, self.entry)
 
 
-def forward_fp8(q, k, v, window: int, sink: int, scale: float, descale=(1.0, 1.0, 1.0), sinks=None):
+def forward_fp8(q, k, v, window: int, sink: int, scale: float, descale=(1.0, 1.0, 1.0), sinks=None,
+                fp8_pv: bool = False):
     """(o bf16, lse) of attention over the dequantised e4m3 inputs descale[0] q, descale[1] k,
-    descale[2] v (fa_fwd_fp8)."""
-    call = Fp8FwdCall(q, k, v, window, sink, scale, descale, sinks)
+    descale[2] v (fa_fwd_fp8; fa_fwd_fp8_pv with ``fp8_pv``)."""
+    call = Fp8FwdCall(q, k, v, window, sink, scale, descale, sinks, fp8_pv)
     call.run()
     return call.o, call.lse
 

@@ -148,19 +148,21 @@ def quantize_fp8(x: torch.Tensor, descale: Optional[float] = None):
 
 
 def flash_swda_with_sink_fp8(q, k, v, window_size, sink_size: int = 0, scale: Optional[float] = None,
-                             descale=(1.0, 1.0, 1.0), sinks=None):
+                             descale=(1.0, 1.0, 1.0), sinks=None, fp8_pv: bool = False):
     """Forward only, FP8 inputs: q [B,Hq,L,D], k/v [B,Hkv,L,D] in torch.float8_e4m3fn standing for
     descale[0] q, descale[1] k, descale[2] v (see quantize_fp8); D is 64 or 128.  Returns o in
     bfloat16: the same attention (window, positional sinks, optional learned sink logits
     `sinks` [Hq]) as flash_swda_with_sink on the dequantised inputs, with Q K^T on the fp8
-    matrix cores.  window_size None means full causal attention.  No autograd: the reference's
-    kernels have no fp8 path (flash_attention_gpt_oss.py:356-383 take 16/32-bit tensors)."""
+    matrix cores.  With ``fp8_pv`` P V runs on them too, on softmax weights rounded to e4m3
+    (a relative error of up to 2^-4 per weight; fa_fwd_fp8_pv in include/fa_gfx950.h).
+    window_size None means full causal attention.  No autograd: the reference's kernels have no
+    fp8 path (flash_attention_gpt_oss.py:356-383 take 16/32-bit tensors)."""
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     _check_shapes(q, k, v)
     if window_size is None:
         window_size = q.shape[2]
-    o, _ = _ops.forward_fp8(q, k, v, int(window_size), int(sink_size), float(scale), descale, sinks)
+    o, _ = _ops.forward_fp8(q, k, v, int(window_size), int(sink_size), float(scale), descale, sinks, fp8_pv)
     return o
 
 

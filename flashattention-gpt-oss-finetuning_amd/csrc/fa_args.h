@@ -104,7 +104,8 @@ __device__ KArgs& args_fresh();  // device code only
 
 // Launchers (return the hipError_t of the launch; launch_bwd_dkdv also launches the sink fold).
 hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
-hipError_t launch_fwd_fp8(const Args& a, int D, int hpw, hipStream_t stream);  // e4m3 q, k, v; bf16 o
+// e4m3 q, k, v; bf16 o; fp8_pv: P V on the fp8 MFMA as well
+hipError_t launch_fwd_fp8(const Args& a, int D, int hpw, bool fp8_pv, hipStream_t stream);
 hipError_t launch_bwd_dq(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
 hipError_t launch_bwd_dkdv(const Args& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_bwd_sink_logits(const Args& a, hipStream_t stream);  // after launch_bwd_dq

@@ -254,7 +254,8 @@ int check_fwd_fp8(const fa_fwd_params* p, float qd, float kd, float vd) {
 
 // The scores are (q_descale k_descale scale) * (q . k) over the stored e4m3 values; O is scaled
 // by v_descale in the kernel's epilogue.
-int run_fwd_fp8(const fa_fwd_params* p, float qd, float kd, float vd, const float* sinks, void* stream) {
+int run_fwd_fp8(const fa_fwd_params* p, float qd, float kd, float vd, const float* sinks, bool fp8_pv,
+                void* stream) {
   const float scale = p->softmax_scale * qd * kd;
   fa::Args a = base_args(p->batch, p->heads_q, p->heads_kv, p->seqlen, p->head_dim, p->window, p->sink, scale);
   a.qsign = scale < 0.f ? 0x80808080u : 0u;
@@ -275,7 +276,7 @@ int run_fwd_fp8(const fa_fwd_params* p, float qd, float kd, float vd, const floa
   a.wh = wh;
   a.wq = wq;
   a.n_qtiles = (a.L + 32 * wq - 1) / (32 * wq);
-  const hipError_t e = fa::launch_fwd_fp8(a, p->head_dim, hpw, static_cast<hipStream_t>(stream));
+  const hipError_t e = fa::launch_fwd_fp8(a, p->head_dim, hpw, fp8_pv, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 
@@ -302,7 +303,15 @@ int fa_fwd_fp8(const fa_fwd_params* p, float q_descale, float k_descale, float v
   const int rc = check_fwd_fp8(p, q_descale, k_descale, v_descale);
   if (rc != FA_OK) return rc;
   if (sinks && !aligned4(sinks)) return FA_ERR_ALIGN;
-  return run_fwd_fp8(p, q_descale, k_descale, v_descale, sinks, stream);
+  return run_fwd_fp8(p, q_descale, k_descale, v_descale, sinks, false, stream);
+}
+
+int fa_fwd_fp8_pv(const fa_fwd_params* p, float q_descale, float k_descale, float v_descale, const float* sinks,
+                  void* stream) {
+  const int rc = check_fwd_fp8(p, q_descale, k_descale, v_descale);
+  if (rc != FA_OK) return rc;
+  if (sinks && !aligned4(sinks)) return FA_ERR_ALIGN;
+  return run_fwd_fp8(p, q_descale, k_descale, v_descale, sinks, true, stream);
 }
 
 int fa_fwd_sinks(const fa_fwd_params* p, const float* sinks, void* stream) {
@@ -455,8 +464,8 @@ const char* fa_strerror(int status) {
     case FA_OK: return "ok";
     case FA_ERR_NULL: return "a required pointer is NULL";
     case FA_ERR_SHAPE: return "invalid shape: batch, heads and seqlen must be >= 1 and heads_q % heads_kv == 0";
-    case FA_ERR_HEAD_DIM: return "head_dim must be one of 16, 32, 64, 128 (64 or 128 for fa_fwd_fp8)";
-    case FA_ERR_DTYPE: return "dtype must be FA_DTYPE_BF16 or FA_DTYPE_F16 (FA_DTYPE_FP8_E4M3 for fa_fwd_fp8)";
+    case FA_ERR_HEAD_DIM: return "head_dim must be one of 16, 32, 64, 128 (64 or 128 for fa_fwd_fp8*)";
+    case FA_ERR_DTYPE: return "dtype must be FA_DTYPE_BF16 or FA_DTYPE_F16 (FA_DTYPE_FP8_E4M3 for fa_fwd_fp8*)";
     case FA_ERR_ALIGN: return "tensors must be 16-byte aligned with non-negative strides that are multiples of 16 bytes (lse: 4-byte aligned, non-negative strides)";
     case FA_ERR_MASK: return "window < 1 and sink < 1 leave every query row fully masked";
     case FA_ERR_WORKSPACE: return "workspace is NULL, not 256-byte aligned or smaller than fa_bwd_workspace_bytes()";

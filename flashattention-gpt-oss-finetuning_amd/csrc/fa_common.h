@@ -124,6 +124,19 @@ __device__ __forceinline__ void fp8x16_to_bf16(u32x4 x, u32x4& lo, u32x4& hi) {
   hi = u32x4{o[4], o[5], o[6], o[7]};
 }
 
+// Four fp32 values -> four e4m3 bytes, in order (v_cvt_pk_fp8_f32: round to nearest even, checked
+// on hardware against the OCP encoding for every finite value; |x| <= 448 assumed).
+__device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
+}
+// v_permlane32_swap: lanes 32..63 of x trade values with lanes 0..31 of y (checked on hardware).
+__device__ __forceinline__ void swap_halves(uint32_t& x, uint32_t& y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+  x = r[0];
+  y = r[1];
+}
+
 // Eight fp32 C values -> one 16-byte B operand.
 template <typename E>
 __device__ __forceinline__ u32x4 pack8(const float* x) {
@@ -198,6 +211,16 @@ __device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride, int col
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t* p) {
   const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// ds_read_b64_tr_b8 (gfx950): within each group of 16 lanes, output lane i, byte j is byte i % 8 of
+// the 8 bytes addressed by lane 2j + i / 8 of the group.  (Checked on hardware by an in-bounds
+// probe.)  Reading 8 rows x 16 byte columns of a row-major LDS tile this way hands each lane one
+// column and 8 consecutive rows.
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x2 ds_read_tr8(const uint16_t* p) {
+  const i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2*)(p));
   return __builtin_bit_cast(u32x2, v);
 }
 

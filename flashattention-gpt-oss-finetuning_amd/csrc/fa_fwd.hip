@@ -26,9 +26,6 @@ namespace fa {
 
 constexpr float kRescaleGap = 8.f;  // log2 units: P stays <= 256 between rescales
 
-// One 32-key half [ks0, ks0 + 32) of the keys -- swizzled [32][D] K and V tiles in LDS at Kl, Vl --
-// for the HPW heads of a wave whose 32 rows start at qw (this lane's row q): masked scores, the
-// online-softmax update of (m2, lsum, acc) and O^T += V^T P^T.
 // Additive masks of the partially masked halves that recur on every tile, built once per
 // workgroup in LDS (fwd_patterns): lane l's 16 values at [(e / 4) * 64 + l] * 4 + e % 4 of pattern
 // p = 0 (the diagonal half, qw - ks0 = 0), 1 and 2 (the window-edge halves, qw - ks0 = e1 and
@@ -67,16 +64,17 @@ __device__ __forceinline__ void fwd_patterns(float* pat, int W, int S) {
 // Q fragments per head and lane: 16 bytes each, head-dim slice [hf*D/2 + 8ks, +8) for 16-bit
 // inputs; for e4m3 inputs, fragment f holds bytes [64 (f / 2) + 32 hf + 16 (f % 2), +16) of the
 // row, the operand layout of the fp8 MFMA.
-template <int D, bool F8>
+// F8 = 0: 16-bit inputs; 1: e4m3 inputs, Q K^T on the fp8 MFMA; 2: also P V on the fp8 MFMA.
+template <int D, int F8>
 constexpr int kQFrags = F8 ? D / 32 : D / 16;
 
-template <typename E, int D, int HPW, bool F8>
-__device__ __forceinline__ void fwd_half(const Args& a, const uint16_t* Kl, const uint16_t* Vl, int ks0, int qw, int q,
-                                         const u32x4 (&qf)[HPW][kQFrags<D, F8>], float (&m2)[HPW], float (&lsum)[HPW],
-                                         f32x16 (&acc)[HPW][D >= 32 ? D / 32 : 1], const float* pat,
-                                         EdgeOffsets eo) {
+// Masked scores S^T = K Q^T of one 32-key half [ks0, ks0 + 32) -- the swizzled K tile at Kl --
+// for the HPW heads of a wave whose 32 rows start at qw (this lane's row q).
+template <typename E, int D, int HPW, int F8>
+__device__ __forceinline__ void half_scores(const Args& a, const uint16_t* Kl, int ks0, int qw, int q,
+                                            const u32x4 (&qf)[HPW][kQFrags<D, F8>], const float* pat,
+                                            EdgeOffsets eo, f32x16 (&s)[HPW]) {
   constexpr int KS = kQFrags<D, F8>;
-  constexpr int DB = D >= 32 ? D / 32 : 1;
   const int lane = threadIdx.x & 63;
   const int r32 = lane & 31, hf = lane >> 5;
   const int W = a.W, S = a.S;
@@ -86,7 +84,6 @@ __device__ __forceinline__ void fwd_half(const Args& a, const uint16_t* Kl, cons
   // of row q; with dq0 = q - ks0 - 4hf the test is one unsigned compare,
   // allowed = (dq0 - off) < lim, lim = W for ordinary keys and 2^31 for sink keys (any
   // q >= k).  Which form applies is wave-uniform.
-  f32x16 s[HPW];
   // Head by head: head 0's scores are complete while head 1's MFMAs are still in the
   // pipe, and head 0's softmax (VALU) overlaps them.
   u32x4 kf[KS];
@@ -144,6 +141,18 @@ __device__ __forceinline__ void fwd_half(const Args& a, const uint16_t* Kl, cons
     }
     qk(bias);
   }
+}
+
+// One 32-key half of the 16-bit P V path: masked scores, the online-softmax update of (m2, lsum,
+// acc) and O^T += V^T P^T, V^T read transposed from the swizzled [32][D] 16-bit V tile at Vl.
+template <typename E, int D, int HPW, int F8>
+__device__ __forceinline__ void fwd_half(const Args& a, const uint16_t* Kl, const uint16_t* Vl, int ks0, int qw, int q,
+                                         const u32x4 (&qf)[HPW][kQFrags<D, F8>], float (&m2)[HPW], float (&lsum)[HPW],
+                                         f32x16 (&acc)[HPW][D >= 32 ? D / 32 : 1], const float* pat,
+                                         EdgeOffsets eo) {
+  constexpr int DB = D >= 32 ? D / 32 : 1;
+  f32x16 s[HPW];
+  half_scores<E, D, HPW, F8>(a, Kl, ks0, qw, q, qf, pat, eo, s);
   // V^T operands of O^T += V^T P^T, shared by the heads: read transposed from the
   // row-major V block, keys in the row order of the P^T C tile.
   u32x4 vf[DB][2];
@@ -186,17 +195,105 @@ __device__ __forceinline__ void fwd_half(const Args& a, const uint16_t* Kl, cons
   }
 }
 
-// F8: q, k, v hold OCP e4m3 values (fa_fwd_fp8); Q K^T runs on the fp8 MFMA, V is widened to
-// bf16 (exactly) on its way into LDS so that P V is the 16-bit path's, and O (type E = BF16) is
-// scaled by a.oscale, the dequantisation factor of V.
-template <typename E, int D, int HPW, bool F8>
+// P V on the fp8 matrix cores (F8 = 2): one 64-key block [kb, kb + 64) -- swizzled e4m3 K and V
+// tiles at Kl, Vl, both laid out like 16-bit rows of D / 2 elements -- for the HPW heads of the
+// wave.  v_mfma_scale_f32_32x32x64 reduces over 64 keys, so both halves' scores come first (a half
+// with need[sb] false lies outside the wave's rows and counts as masked), then one online-softmax
+// update over the 64 keys.
+//  * P = 2^(s c - m2 + kP8Shift) is rounded to e4m3.  m2 moves when a row's maximum exceeds it by
+//    more than kP8Gap, so P <= 2^(kP8Gap + kP8Shift) = 256 < 448, the e4m3 maximum; weights down
+//    to 2^-(kP8Shift + 9) of the row maximum's stay representable.
+//  * The row sum adds the rounded P that the product uses, so every row's weights sum to one.  It
+//    runs on the matrix cores too: a product with an all-ones A operand leaves the sum of row q's
+//    64 weights in every register of column q, accumulated in lacc like O^T in acc.
+//  * Packed word w of lane (q, hf) holds P of keys 8w + 4hf + 0..3 (the C layout of S^T); one
+//    v_permlane32_swap per word pair turns that into keys 16m + 8hf + 0..7 in words 2m, 2m + 1,
+//    runs of 8 keys that ds_read_b64_tr_b8 reads from the row-major V tile as the A operand.
+constexpr float kP8Gap = 4.f, kP8Shift = 4.f;
+
+template <int D, int HPW>
+__device__ __forceinline__ void fwd_block_pv8(const Args& a, const uint16_t* Kl, const uint16_t* Vl, int kb,
+                                              const bool (&need)[2], int qw, int q,
+                                              const u32x4 (&qf)[HPW][D / 32], float (&m2)[HPW],
+                                              f32x16 (&lacc)[HPW], f32x16 (&acc)[HPW][D / 32], const float* pat,
+                                              EdgeOffsets eo) {
+  constexpr int DB = D / 32;
+  const int lane = threadIdx.x & 63;
+  f32x16 s[2][HPW];
+#pragma unroll
+  for (int sb = 0; sb < 2; ++sb)
+    if (need[sb]) half_scores<BF16, D, HPW, 2>(a, Kl + 32 * sb * (D / 2), kb + 32 * sb, qw, q, qf, pat, eo, s[sb]);
+  // V^T operands, shared by the heads: lane (r, hf) byte 8m + t is V[16m + 8hf + t][32db + r].
+  // Lane 2j + b of 16-lane group g addresses key 16m + 8(g / 2) + j, bytes 32db + 16(g % 2) + 8b.
+  u32x4 vf[DB][2];
+  {
+    const int g = lane >> 4, sl = lane & 15;
+    const int key = 8 * (g >> 1) + (sl >> 1);
+    const int col = 8 * (g & 1) + 4 * (sl & 1);  // in 16-bit units
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const u32x2 x = ds_read_tr8(Vl + swz_off<D / 2>(key + 16 * m, 16 * db + col));
+        vf[db][m / 2][2 * (m % 2)] = x[0];
+        vf[db][m / 2][2 * (m % 2) + 1] = x[1];
+      }
+  }
+#pragma unroll
+  for (int h = 0; h < HPW; ++h) {
+    float m = kNegInf;
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+      if (need[sb])
+#pragma unroll
+        for (int e = 0; e < 16; ++e) m = fmaxf(m, s[sb][h][e]);
+    const float mx = max_halves(m) * a.c;
+    if (wave_any(mx > m2[h] + kP8Gap)) {
+      const float mnew = fmaxf(m2[h], mx);
+      const float alpha = mnew == kNegInf ? 1.f : fast_exp2(m2[h] - mnew);
+      m2[h] = mnew;
+      lacc[h] *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[h][db] *= alpha;
+    }
+    const float ms = (m2[h] == kNegInf ? 0.f : m2[h]) - kP8Shift;
+    uint32_t pw[8];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      if (need[sb]) {
+        float sv[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sv[e] = fast_exp2(fmaf(s[sb][h][e], a.c, -ms));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) pw[4 * sb + w] = pack4_fp8(sv[4 * w], sv[4 * w + 1], sv[4 * w + 2], sv[4 * w + 3]);
+      } else {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) pw[4 * sb + w] = 0u;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) swap_halves(pw[2 * j], pw[2 * j + 1]);
+    const u32x4 plo = {pw[0], pw[1], pw[2], pw[3]}, phi = {pw[4], pw[5], pw[6], pw[7]};
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[h][db] = mfma_fp8(vf[db][0], vf[db][1], plo, phi, acc[h][db]);
+    const u32x4 ones = {0x38383838u, 0x38383838u, 0x38383838u, 0x38383838u};  // e4m3 1.0
+    lacc[h] = mfma_fp8(ones, ones, plo, phi, lacc[h]);
+  }
+}
+
+
+// F8 (e4m3 q, k, v; fa_fwd_fp8 and fa_fwd_fp8_pv): Q K^T runs on the fp8 MFMA and O (type E =
+// BF16) is scaled by a.oscale, the dequantisation factor of V.  With F8 = 1, V is widened to bf16
+// (exactly) on its way into LDS and P V is the 16-bit path's; with F8 = 2, V stays e4m3 in LDS and
+// P V runs on the fp8 MFMA too (fwd_block_pv8).
+template <typename E, int D, int HPW, int F8>
 __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   constexpr int BN = 64;                   // keys per LDS block
   constexpr int KS = kQFrags<D, F8>;       // 16-byte Q fragments per head and lane
   constexpr int DB = D >= 32 ? D / 32 : 1; // 32-row C tiles of O^T
   constexpr int EB = F8 ? 1 : 2;           // bytes per input element
   constexpr int KBUF = BN * D * EB / 2;    // K block in LDS (16-bit units), swizzled row-major [key][d]
-  constexpr int BUF = KBUF + BN * D;       // K, then V as 16-bit values, swizzled row-major [key][d]
+  constexpr int BUF = KBUF + (F8 == 2 ? KBUF : BN * D);  // K, then V (16-bit unless F8 = 2), swizzled [key][d]
   constexpr int CPR = D * EB / 16;         // 16-byte chunks per K (or V) row in memory
   constexpr int CPB = BN * CPR;            // 16-byte chunks per 64-key block of K (or V)
   constexpr int NK = (CPB + 255) / 256;    // chunks per thread
@@ -286,8 +383,8 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   const uint32_t off_k0 = uint32_t(int64_t(row0) * a.sk[2] * EB + 16 * col0);
   const uint32_t off_v0 = uint32_t(int64_t(row0) * a.sv[2] * EB + 16 * col0);
   const int off_l0 = F8 ? swz_off<D / 2>(row0, 8 * col0) : swz_off<D>(row0, 8 * col0);
-  const int off_lv0 = F8 ? swz_off<D>(row0, 16 * col0) : off_l0;
-  const int off_lv1 = F8 ? swz_off<D>(row0, 16 * col0 + 8) : off_l0;
+  const int off_lv0 = F8 == 1 ? swz_off<D>(row0, 16 * col0) : off_l0;
+  const int off_lv1 = F8 == 1 ? swz_off<D>(row0, 16 * col0 + 8) : off_l0;
   const uint32_t bk = uint32_t(EB * a.sk[2]), bv = uint32_t(EB * a.sv[2]);  // bytes per key row
 
   // the recurring masks (made visible by the barrier before the first key block)
@@ -325,10 +422,12 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
 
   float m2[HPW], lsum[HPW];
   f32x16 acc[HPW][DB];
+  f32x16 lacc[F8 == 2 ? HPW : 1];  // F8 = 2: row sums from the matrix cores (fwd_block_pv8)
 #pragma unroll
   for (int h = 0; h < HPW; ++h) {
     m2[h] = kNegInf;
     lsum[h] = 0.f;
+    if constexpr (F8 == 2) lacc[h] = f32x16{};
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[h][db] = f32x16{};
   }
@@ -361,7 +460,10 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
 #pragma unroll
     for (int it = 0; it < NK; ++it) {
       if (ALL_ON || tid + 256 * it < CPB) {
-        if constexpr (F8) {
+        if constexpr (F8 == 2) {
+          st16(Kl + off_l0 + RSTEP * (D / 2) * it, kreg[it]);
+          st16(Vl + off_l0 + RSTEP * (D / 2) * it, vreg[it]);
+        } else if constexpr (F8) {
           st16(Kl + off_l0 + RSTEP * (D / 2) * it, kreg[it]);
           u32x4 v0, v1;
           fp8x16_to_bf16(vreg[it], v0, v1);
@@ -393,12 +495,17 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     if (wave_active) {
       const uint16_t* Kl = lds + (i & 1) * BUF;
       const uint16_t* Vl = Kl + KBUF;
+      if constexpr (F8 == 2) {
+        const bool need[2] = {wave_needs(kb, qw, L, W, S), wave_needs(kb + 32, qw, L, W, S)};
+        if (need[0] || need[1]) fwd_block_pv8<D, HPW>(a, Kl, Vl, kb, need, qw, q, qf, m2, lacc, acc, pat, eo);
+      } else {
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        const int ks0 = kb + 32 * sb;
-        if (!wave_needs(ks0, qw, L, W, S)) continue;
-        fwd_half<E, D, HPW, F8>(a, Kl + 32 * sb * (KBUF / BN), Vl + 32 * sb * D, ks0, qw, q, qf, m2, lsum, acc, pat,
-                                eo);
+        for (int sb = 0; sb < 2; ++sb) {
+          const int ks0 = kb + 32 * sb;
+          if (!wave_needs(ks0, qw, L, W, S)) continue;
+          fwd_half<E, D, HPW, F8>(a, Kl + 32 * sb * (KBUF / BN), Vl + 32 * sb * D, ks0, qw, q, qf, m2, lsum, acc,
+                                  pat, eo);
+        }
       }
     }
     if (more) sstore((i + 1) & 1);
@@ -415,7 +522,11 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   if (!wave_active) continue;
 #pragma unroll
   for (int h = 0; h < HPW; ++h) {
-    float lt = sum_halves(lsum[h]);
+    float lt;
+    if constexpr (F8 == 2)  // the whole row's sum, of P scaled by 2^kP8Shift
+      lt = lacc[h][0] * (1.f / (1 << int(kP8Shift)));
+    else
+      lt = sum_halves(lsum[h]);
     if (q >= L) continue;
     float mt = m2[h], r = 1.f;
     KArgs& A = args_fresh();
@@ -429,7 +540,8 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
       mt = mn;
     }
     float inv = lt > 0.f ? r / lt : 0.f;
-    if constexpr (F8) inv *= A.oscale;
+    if constexpr (F8 == 2) inv *= A.oscale / (1 << int(kP8Shift));
+    else if constexpr (F8) inv *= A.oscale;
     char* op = reinterpret_cast<char*>(A.o_out) + 2 * slice_off(A.so_out, b, hw + h, t.row + q);
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
@@ -437,6 +549,14 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
       float ov[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) ov[e] = acc[h][db][e] * inv;
+      if constexpr (F8 == 2) {  // C row 8j + 4hf + i is head dim 32db + 8j + 4hf + i
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const u32x2 w = {E::pack2(ov[4 * j], ov[4 * j + 1]), E::pack2(ov[4 * j + 2], ov[4 * j + 3])};
+          *reinterpret_cast<u32x2*>(op + 2 * (32 * db + 8 * j + 4 * hf)) = w;
+        }
+        continue;
+      }
       const int d0 = 32 * db + (D >= 32 ? 16 * hf : 0);
       st16(op + 2 * d0, pack8<E>(ov));
       st16(op + 2 * (d0 + 8), pack8<E>(ov + 8));
@@ -462,7 +582,7 @@ static int fwd_resident_per_cu() {
   return cached;
 }
 
-template <typename E, int D, int HPW, bool F8 = false>
+template <typename E, int D, int HPW, int F8 = 0>
 static hipError_t launch_fwd_h(const Args& a, hipStream_t stream) {
   const int n_tiles = a.n_qtiles * (a.B * a.Hq / (HPW * a.wh));
   int dev = 0, cus = 0;
@@ -497,11 +617,16 @@ hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stre
 }
 
 // e4m3 inputs, bf16 output: D = 64 shares K/V fragments between two heads per wave where the
-// group size allows, D = 128 has one head per wave.
-hipError_t launch_fwd_fp8(const Args& a, int D, int hpw, hipStream_t stream) {
-  if (D == 64) return hpw == 2 ? launch_fwd_h<BF16, 64, 2, true>(a, stream) : launch_fwd_h<BF16, 64, 1, true>(a, stream);
-  if (D == 128 && hpw == 1) return launch_fwd_h<BF16, 128, 1, true>(a, stream);
+// group size allows, D = 128 has one head per wave.  fp8_pv selects P V on the fp8 MFMA.
+template <int F8>
+static hipError_t launch_fwd_fp8_m(const Args& a, int D, int hpw, hipStream_t stream) {
+  if (D == 64) return hpw == 2 ? launch_fwd_h<BF16, 64, 2, F8>(a, stream) : launch_fwd_h<BF16, 64, 1, F8>(a, stream);
+  if (D == 128 && hpw == 1) return launch_fwd_h<BF16, 128, 1, F8>(a, stream);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_fwd_fp8(const Args& a, int D, int hpw, bool fp8_pv, hipStream_t stream) {
+  return fp8_pv ? launch_fwd_fp8_m<2>(a, D, hpw, stream) : launch_fwd_fp8_m<1>(a, D, hpw, stream);
 }
 
 }  // namespace fa

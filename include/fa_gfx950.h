@@ -37,10 +37,10 @@
 extern "C" {
 #endif
 
-#define FA_GFX950_VERSION 10300 /* 1.3.0 */
+#define FA_GFX950_VERSION 10400 /* 1.4.0 */
 
 /* Element types of q/k/v/o/dout/dq/dk/dv.  All of them share one type per call, except in
- * fa_fwd_fp8: FA_DTYPE_FP8_E4M3 means OCP float8 e4m3 q, k, v and a bf16 o. */
+ * fa_fwd_fp8 and fa_fwd_fp8_pv: FA_DTYPE_FP8_E4M3 means OCP float8 e4m3 q, k, v and a bf16 o. */
 enum fa_dtype { FA_DTYPE_BF16 = 1, FA_DTYPE_F16 = 2, FA_DTYPE_FP8_E4M3 = 3 };
 
 enum fa_status {
@@ -186,6 +186,16 @@ int fa_bwd_varlen(const fa_bwd_params* p, const int32_t* cu_seqlens, int32_t tot
  * full-causal layers, D = 128), forward only. */
 int fa_fwd_fp8(const fa_fwd_params* p, float q_descale, float k_descale, float v_descale, const float* sinks,
                void* stream);
+
+/* fa_fwd_fp8 with P V on the fp8 matrix cores as well (same arguments, checks and outputs).  The
+ * softmax weights are rounded to e4m3 before the product.  A row's weights still sum to one (the
+ * row sum adds the rounded values); a weight of at least 2^-10 of the row's largest carries a
+ * relative rounding error of at most 2^-4, a smaller one an absolute error of at most 2^-14 of the
+ * largest.  So o moves by at most 2^-4 of the weighted spread of v around o plus that absolute
+ * term (the bound the tests check), and lse by at most -ln(1 - 2^-4) from fa_fwd_fp8's.  Same reference counterpart as
+ * fa_fwd_fp8 (none: flash_attention_gpt_oss.py:356-383 takes 16/32-bit tensors only). */
+int fa_fwd_fp8_pv(const fa_fwd_params* p, float q_descale, float k_descale, float v_descale, const float* sinks,
+                  void* stream);
 
 /* Host-only argument checks used by fa_fwd / fa_bwd (no HIP call is made). */
 int fa_check_fwd(const fa_fwd_params* p);

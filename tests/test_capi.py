@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_strerror():
     L = _lib.lib()
-    assert L.fa_version() == 10300
+    assert L.fa_version() == 10400
     codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10]
     texts = [_lib.strerror(c) for c in codes]
     assert len(set(texts)) == len(codes)
@@ -247,16 +247,18 @@ def test_varlen_entry_points_reject_before_any_hip_call():
                            ctypes.c_size_t(0), None) == _lib.FA_ERR_WORKSPACE
 
 
-def test_fp8_entry_point_rejects_before_any_hip_call():
-    """fa_fwd_fp8's own checks: e4m3 dtype code, D in {64, 128}, 16-byte strides of the e4m3
-    tensors (8-element strides of the bf16 output), finite dequantisation factors."""
+@pytest.mark.parametrize("entry", ["fa_fwd_fp8", "fa_fwd_fp8_pv"])
+def test_fp8_entry_point_rejects_before_any_hip_call(entry):
+    """The fp8 entry points' own checks: e4m3 dtype code, D in {64, 128}, 16-byte strides of the
+    e4m3 tensors (8-element strides of the bf16 output), finite dequantisation factors."""
     L = _lib.lib()
     F8 = _lib.FA_DTYPE_FP8_E4M3
+    fn = getattr(L, entry)
 
     def call(p, qd=1.0, kd=1.0, vd=1.0, sinks=None):
-        return L.fa_fwd_fp8(ctypes.byref(p), qd, kd, vd, sinks, None)
+        return fn(ctypes.byref(p), qd, kd, vd, sinks, None)
 
-    assert L.fa_fwd_fp8(None, 1.0, 1.0, 1.0, None, None) == _lib.FA_ERR_NULL
+    assert fn(None, 1.0, 1.0, 1.0, None, None) == _lib.FA_ERR_NULL
     assert call(_fwd_params(dtype=F8, v=None)) == _lib.FA_ERR_NULL
     assert call(_fwd_params()) == _lib.FA_ERR_DTYPE  # bf16 code
     assert call(_fwd_params(dtype=F8, head_dim=32)) == _lib.FA_ERR_HEAD_DIM

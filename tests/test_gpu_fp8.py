@@ -15,6 +15,10 @@ internal precision (an in-bounds probe of one 32x32x64 product measured errors o
 the result's magnitude, against about 1e-7 for fp32 sums), which moves scores of magnitude ~30
 by ~1e-3, so that check's bound is 1e-2 on LSE and 1e-2 + 1e-2 |O| on O -- tighter than the
 oracle bar.
+
+fa_fwd_fp8_pv (P V on the fp8 matrix cores as well) rounds the softmax weights to e4m3; its tests,
+at the end of this file, check the error bound that rounding allows (derived there) on the same
+cases, against the same oracle.
 """
 import math
 
@@ -143,3 +147,113 @@ def test_fp8_public_api_and_errors(gpu):
         fa.flash_swda_with_sink_fp8(q8.float().to(torch.bfloat16), k8, v8, 16, 0)
     with pytest.raises(AssertionError, match="Key and Value shapes must be the same"):
         fa.flash_swda_with_sink_fp8(q8, k8, v8[:, :1], 16, 0)
+
+
+# ---- fa_fwd_fp8_pv: P V on the fp8 matrix cores as well --------------------------------------
+#
+# The kernel rounds the softmax weights P (scaled so that the largest of a row is >= 16) to e4m3
+# before the product and divides by the sum of the rounded weights, so with p the exact
+# normalised weights and O the oracle's output,
+#     O_pv - O = sum_k (P~_k - P_k)(v_k - O) / sum_k P~_k.
+# e4m3 rounding moves a weight >= 2^-6 by at most 2^-4 of itself and a smaller one by at most
+# 2^-10 (half the subnormal spacing 2^-9); sum P~ >= (1 - 2^-4) sum P and sum P >= 16.  Hence
+#     |O_pv - O| <= 2^-4 / (1 - 2^-4) * sum_k p_k |v_k - O| + n * 2^-14 * max_k |v_k - O|
+# over the n allowed keys of the row; sum_k p_k |v_k - O| <= p @ |v| + |O| and
+# max_k |v_k - O| <= max_k |v_k| + |O| make both terms cheap to evaluate.  The log-sum-exp moves
+# by at most -ln(1 - 2^-4) + n 2^-14 / 16.  On top of those, the test keeps the 16-bit bar
+# (2e-2 + 2e-2 |ref|) for the Q K^T sums and the bf16 output.  A wrong key or head-dim order in
+# the product would move O by about the whole spread and fail the first term (0.07 of it).
+
+
+def pv_bound(q8, k8, v8, ds, W, S, scale, ro, sinks=None):
+    qf, kf, vf = (x.float().cpu() * d for x, d in zip((q8, k8, v8), ds))
+    B, Hq, L, D = qf.shape
+    g = Hq // kf.shape[1]
+    kf, vf = naive.expand_kv(kf, g), naive.expand_kv(vf, g)
+    allowed = naive.allowed_mask(L, W, S)
+    s = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) * scale
+    s = s.masked_fill(~allowed, float("-inf"))
+    if sinks is not None:
+        sl = sinks.float().cpu().view(1, Hq, 1, 1).expand(B, Hq, L, 1)
+        p = torch.softmax(torch.cat([s, sl], dim=-1), dim=-1)[..., :L]
+    else:
+        p = torch.softmax(s, dim=-1)
+    o = ro.float().cpu().abs()
+    spread = torch.matmul(p, vf.abs()) + o
+    n = allowed.sum(-1).view(1, 1, L, 1).float()
+    vmax = vf.abs().amax(dim=2, keepdim=True)  # over all keys: an upper bound of the allowed ones
+    bound = 0.07 * spread + n * 2.0 ** -14 * (vmax + o)
+    lse_bound = 0.0645 + n[..., 0] * 2.0 ** -18
+    return bound, lse_bound
+
+
+def assert_pv_close(o, lse, ro, rlse, bound, lse_bound):
+    err = (o.float().cpu() - ro.float().cpu()).abs()
+    lim = bound + 2e-2 + 2e-2 * ro.float().cpu().abs()
+    assert bool((err <= lim).all()), f"O: worst excess {float((err - lim).max()):.4g}, max err {float(err.max()):.4g}"
+    lerr = (lse.float().cpu() - rlse.float().cpu()).abs()
+    llim = lse_bound + 2e-2 + 2e-2 * rlse.float().cpu().abs()
+    assert bool((lerr <= llim).all()), f"LSE: max err {float(lerr.max()):.4g}"
+    # rounding errors of independent weights mostly cancel: the typical error stays far below the bound
+    assert float(err.mean()) < 0.25 * float(lim.mean()), (float(err.mean()), float(lim.mean()))
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}-H{c[1]}x{c[2]}-L{c[3]}-D{c[4]}-W{c[5]}-S{c[6]}" for c in CASES])
+def test_fp8_pv_forward_parity(gpu, case):
+    B, Hq, Hkv, L, D, W, S = case
+    ops = load_mod("_ops")
+    (q8, qd), (k8, kd), (v8, vd) = fp8_inputs(B, Hq, Hkv, L, D, seed=L)
+    sc = 1.0 / math.sqrt(D)
+    print(f"fp8_pv case {case}", flush=True)
+    o, lse = ops.forward_fp8(q8, k8, v8, W, S, sc, (qd, kd, vd), fp8_pv=True)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.bfloat16 and lse.dtype == torch.float32
+    ro, rlse = reference(q8, k8, v8, (qd, kd, vd), W, S, sc)
+    bound, lse_bound = pv_bound(q8, k8, v8, (qd, kd, vd), W, S, sc, ro)
+    assert_pv_close(o, lse, ro, rlse, bound, lse_bound)
+
+
+def test_fp8_pv_single_key_rows_are_exact(gpu):
+    """W = 1, S = 0: every row sees one key, whose rounded weight divides out, so O is that key's
+    value row whatever the rounding of P -- up to one fp32 rounding of the normalisation, which can
+    flip the bf16 rounding of O by one unit (2^-8 relative)."""
+    ops = load_mod("_ops")
+    B, Hq, Hkv, L, D = 1, 8, 2, 200, 128
+    (q8, qd), (k8, kd), (v8, vd) = fp8_inputs(B, Hq, Hkv, L, D, seed=21)
+    o, _ = ops.forward_fp8(q8, k8, v8, 1, 0, 1.0 / math.sqrt(D), (qd, kd, vd), fp8_pv=True)
+    torch.cuda.synchronize()
+    want = naive.expand_kv(v8.float() * vd, Hq // Hkv).to(torch.bfloat16).float()
+    err = (o.float() - want).abs()
+    assert bool((err <= 2.0 ** -8 * want.abs()).all()), float(err.max())
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_fp8_pv_learned_sinks_and_negative_scale(gpu, D):
+    ops = load_mod("_ops")
+    B, Hq, Hkv, L, W, S = 1, 8, 2, 333, 100, 4
+    (q8, qd), (k8, kd), (v8, vd) = fp8_inputs(B, Hq, Hkv, L, D, seed=D)
+    g = torch.Generator().manual_seed(7)
+    sinks = (2.0 * torch.randn(Hq, generator=g)).cuda()
+    sc = -0.7 / math.sqrt(D)
+    o, lse = ops.forward_fp8(q8, k8, v8, W, S, sc, (qd, kd, vd), sinks, fp8_pv=True)
+    torch.cuda.synchronize()
+    ro, rlse = reference(q8, k8, v8, (qd, kd, vd), W, S, sc, sinks)
+    bound, lse_bound = pv_bound(q8, k8, v8, (qd, kd, vd), W, S, sc, ro, sinks)
+    assert_pv_close(o, lse, ro, rlse, bound, lse_bound)
+
+
+def test_fp8_pv_blhd_layout_determinism_and_api(gpu):
+    fa = load_pkg()
+    ops = load_mod("_ops")
+    B, Hq, Hkv, L, D, W, S = 2, 8, 4, 160, 64, 64, 2
+    (q8, qd), (k8, kd), (v8, vd) = fp8_inputs(B, Hq, Hkv, L, D, seed=11)
+    sc = 1.0 / math.sqrt(D)
+    o1, l1 = ops.forward_fp8(q8, k8, v8, W, S, sc, (qd, kd, vd), fp8_pv=True)
+    o2, l2 = ops.forward_fp8(q8, k8, v8, W, S, sc, (qd, kd, vd), fp8_pv=True)
+    qt, kt, vt = (x.transpose(1, 2).contiguous().transpose(1, 2) for x in (q8, k8, v8))
+    o3, l3 = ops.forward_fp8(qt, kt, vt, W, S, sc, (qd, kd, vd), fp8_pv=True)
+    o4 = fa.flash_swda_with_sink_fp8(q8, k8, v8, W, S, descale=(qd, kd, vd), fp8_pv=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    assert torch.equal(o1, o3) and torch.equal(l1, l3)
+    assert torch.equal(o1, o4)
