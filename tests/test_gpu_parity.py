@@ -146,6 +146,39 @@ def test_edge_cases(gpu, B, Hq, Hkv, L, D, W, S, dtype):
     run_case(B, Hq, Hkv, L, D, W, S, dtype, seed=L + D + W)
 
 
+def _random_cases(n=24, seed=2026):
+    """Shapes drawn from a fixed seed, for combinations the hand-picked cases above do not name:
+    batch 1-3, KV heads 1-4, group sizes 1-8, lengths 1-900 (some not multiples of 32), every
+    head dim, windows from 1 to past L, 0-80 positional sinks, both dtypes, scales around
+    1/sqrt(D).  Sized so that the float32 oracle and the CPU naive reference finish in seconds."""
+    import random
+
+    rng = random.Random(seed)
+    cases = []
+    while len(cases) < n:
+        D = rng.choice([16, 32, 64, 64, 128])
+        Hkv = rng.choice([1, 2, 4])
+        G = rng.choice([1, 2, 3, 4, 8])
+        B = rng.choice([1, 1, 2, 3])
+        L = rng.choice([rng.randint(1, 64), rng.randint(65, 400), rng.randint(401, 900)])
+        W = rng.choice([1, rng.randint(2, 64), rng.randint(65, 300), L, L + rng.randint(1, 100)])
+        S = rng.choice([0, rng.randint(1, 8), rng.randint(9, 80)])
+        if W < 1 and S < 1 or B * Hkv * G * L * L > (1 << 25):
+            continue
+        dtype = rng.choice([BF, FP])
+        scale = rng.uniform(0.5, 1.5) / math.sqrt(D)
+        cases.append(pytest.param(B, Hkv * G, Hkv, L, D, W, S, dtype, scale, len(cases),
+                                  id=f"R{len(cases)}-B{B}-H{Hkv * G}x{Hkv}-L{L}-D{D}-W{W}-S{S}-"
+                                     f"{'bf16' if dtype is BF else 'fp16'}"))
+    return cases
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,D,W,S,dtype,scale,seed", _random_cases())
+def test_random_shapes(gpu, B, Hq, Hkv, L, D, W, S, dtype, scale, seed):
+    print(f"random case B={B} Hq={Hq} Hkv={Hkv} L={L} D={D} W={W} S={S} {dtype} scale={scale:.4g}", flush=True)
+    run_case(B, Hq, Hkv, L, D, W, S, dtype, seed=100 + seed, scale=scale)
+
+
 @pytest.mark.parametrize("scale", [0.05, -0.125, 0.0])
 def test_custom_scales(gpu, scale):
     print(f"case scale={scale}", flush=True)

@@ -102,6 +102,34 @@ def test_learned_sinks_parity(gpu, B, Hq, Hkv, L, D, W, S, dtype):
     run_sinks_case(B, Hq, Hkv, L, D, W, S, dtype, seed=L + D)
 
 
+def _random_sink_cases(n=10, seed=4242):
+    """Learned sink logits on shapes drawn from a fixed seed: every head dim, groups 1-8, lengths
+    1-600, windows from 1 to past L with and without positional sinks, logits of scale 0.5-8."""
+    import random
+
+    rng = random.Random(seed)
+    cases = []
+    while len(cases) < n:
+        D = rng.choice([16, 32, 64, 128])
+        Hkv, G, B = rng.choice([1, 2, 4]), rng.choice([1, 2, 3, 8]), rng.choice([1, 2])
+        L = rng.choice([rng.randint(1, 64), rng.randint(65, 600)])
+        W = rng.choice([1, rng.randint(2, 200), L, L + 7])
+        S = rng.choice([0, 0, rng.randint(1, 40)])
+        if B * Hkv * G * L * L > (1 << 23):
+            continue
+        dtype = rng.choice([BF, FP])
+        sink_scale = rng.choice([0.5, 2.0, 8.0])
+        cases.append(pytest.param(B, Hkv * G, Hkv, L, D, W, S, dtype, sink_scale, len(cases),
+                                  id=f"RS{len(cases)}-B{B}-H{Hkv * G}x{Hkv}-L{L}-D{D}-W{W}-S{S}-x{sink_scale}"))
+    return cases
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,D,W,S,dtype,sink_scale,seed", _random_sink_cases())
+def test_learned_sinks_random_shapes(gpu, B, Hq, Hkv, L, D, W, S, dtype, sink_scale, seed):
+    print(f"random sinks case B={B} Hq={Hq} Hkv={Hkv} L={L} D={D} W={W} S={S} {dtype} x{sink_scale}", flush=True)
+    run_sinks_case(B, Hq, Hkv, L, D, W, S, dtype, seed=200 + seed, sink_scale=sink_scale)
+
+
 def test_learned_sinks_extreme_logits(gpu):
     # a dominant sink (most of the mass on the sink), an irrelevant one, and a zero one
     sinks = torch.tensor([8.0, -40.0, 0.0, 3.0], device="cuda")

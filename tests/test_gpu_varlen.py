@@ -83,6 +83,38 @@ def test_varlen_parity(gpu, cu, Hq, Hkv, D, W, S, dtype):
     run_varlen(cu, Hq, Hkv, D, W, S, dtype, seed=cu[-1] % 97 + D, with_naive=cu[-1] * Hq <= 1 << 16)
 
 
+def _random_varlen_cases(n=8, seed=777):
+    """Packed batches drawn from a fixed seed: 1-6 sequences of 0-500 rows each (empty ones
+    included), every head dim, groups 1-8, windows from 1 to full causal, 0-40 positional sinks,
+    learned sinks on some."""
+    import random
+
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n):
+        lens = [rng.choice([0, rng.randint(1, 40), rng.randint(41, 500)]) for _ in range(rng.randint(1, 6))]
+        if sum(lens) == 0:
+            lens[0] = 17
+        cu = [0]
+        for x in lens:
+            cu.append(cu[-1] + x)
+        D = rng.choice([16, 32, 64, 128])
+        Hkv, G = rng.choice([1, 2, 4]), rng.choice([1, 2, 3, 8])
+        W = rng.choice([1, rng.randint(2, 150), None])
+        S = rng.choice([0, rng.randint(1, 40)])
+        sinks = rng.random() < 0.4
+        dtype = rng.choice([BF, FP])
+        cases.append(pytest.param(cu, Hkv * G, Hkv, D, W, S, dtype, sinks, i,
+                                  id=f"RV{i}-n{len(lens)}-T{cu[-1]}-H{Hkv * G}x{Hkv}-D{D}-W{W}-S{S}"
+                                     f"{'-sinks' if sinks else ''}"))
+    return cases
+
+
+@pytest.mark.parametrize("cu,Hq,Hkv,D,W,S,dtype,sinks,seed", _random_varlen_cases())
+def test_varlen_random_batches(gpu, cu, Hq, Hkv, D, W, S, dtype, sinks, seed):
+    run_varlen(cu, Hq, Hkv, D, W, S, dtype, seed=300 + seed, sinks=sinks, with_naive=cu[-1] * Hq <= 1 << 16)
+
+
 def test_varlen_learned_sinks(gpu):
     run_varlen([0, 250, 700, 701], 8, 1, 64, 128, 0, BF, seed=11, sinks=True)
 
