@@ -257,3 +257,41 @@ def test_fp8_pv_blhd_layout_determinism_and_api(gpu):
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
     assert torch.equal(o1, o3) and torch.equal(l1, l3)
     assert torch.equal(o1, o4)
+
+
+def _random_fp8_cases(n=10, seed=8080):
+    """Shapes drawn from a fixed seed for both fp8 entry points: D 64 or 128, groups 1-8, lengths
+    1-700, windows from 1 to past L, 0-40 positional sinks, learned sinks on some, input scales
+    0.25-4 (so the per-tensor factors differ from 1), the softmax scale around 1/sqrt(D)."""
+    import random
+
+    rng = random.Random(seed)
+    cases = []
+    while len(cases) < n:
+        D = rng.choice([64, 128])
+        Hkv, G, B = rng.choice([1, 2, 4]), rng.choice([1, 2, 3, 8]), rng.choice([1, 2])
+        L = rng.choice([rng.randint(1, 64), rng.randint(65, 700)])
+        W = rng.choice([1, rng.randint(2, 200), L, L + 9])
+        S = rng.choice([0, rng.randint(1, 40)])
+        if B * Hkv * G * L * L > (1 << 23):
+            continue
+        cases.append(pytest.param(B, Hkv * G, Hkv, L, D, W, S, rng.random() < 0.3, rng.choice([0.25, 1.0, 4.0]),
+                                  rng.uniform(0.6, 1.4) / math.sqrt(D), len(cases),
+                                  id=f"RF{len(cases)}-B{B}-H{Hkv * G}x{Hkv}-L{L}-D{D}-W{W}-S{S}"))
+    return cases
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,D,W,S,learned,std,sc,seed", _random_fp8_cases())
+def test_fp8_random_shapes_both_entry_points(gpu, B, Hq, Hkv, L, D, W, S, learned, std, sc, seed):
+    ops = load_mod("_ops")
+    print(f"random fp8 case B={B} Hq={Hq} Hkv={Hkv} L={L} D={D} W={W} S={S} learned={learned} std={std}", flush=True)
+    (q8, qd), (k8, kd), (v8, vd) = fp8_inputs(B, Hq, Hkv, L, D, seed=400 + seed, std=std)
+    sinks = (2.0 * torch.randn(Hq, generator=torch.Generator().manual_seed(seed))).cuda() if learned else None
+    o, lse = ops.forward_fp8(q8, k8, v8, W, S, sc, (qd, kd, vd), sinks)
+    op, lp = ops.forward_fp8(q8, k8, v8, W, S, sc, (qd, kd, vd), sinks, fp8_pv=True)
+    torch.cuda.synchronize()
+    ro, rlse = reference(q8, k8, v8, (qd, kd, vd), W, S, sc, sinks)
+    assert_close("O", o, ro)
+    assert_close("LSE", lse, rlse)
+    bound, lse_bound = pv_bound(q8, k8, v8, (qd, kd, vd), W, S, sc, ro, sinks)
+    assert_pv_close(op, lp, ro, rlse, bound, lse_bound)
