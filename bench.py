@@ -264,6 +264,35 @@ def varlen_measure(steps, warmup, seqs=VARLEN_SEQS):
             "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s"}
 
 
+def shard_proxy_measure(steps, warmup, name="c2", parts=8):
+    """One GPU's share of `name` split over `parts` GPUs by KV-head groups (zero communication:
+    dK/dV reduce only inside a group): the same fwd + bwd on Hq / parts query heads and
+    Hkv / parts KV heads, seq_len and everything else unchanged.  `value` is the device
+    throughput of the three kernels (their HIP-event times summed, as time_kernels measures
+    them); the autograd step is reported beside it, and at this size it is bound by the host's
+    enqueue cost rather than the GPU."""
+    import torch
+
+    fa = _pkg()
+    flops_mod = _mod("flops")
+    cfg = dict(CONFIGS[name])
+    cfg["Hq"] //= parts
+    cfg["Hkv"] //= parts
+    dev = torch.device("cuda", 0)
+    q, k, v, do = make_inputs(cfg, dev)
+    t = time_steps(fa, cfg, q, k, v, do, steps, warmup)
+    kt = time_kernels(cfg, q, k, v, do)
+    wl = flops_mod.Workload(cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"], cfg["D"], cfg["W"], cfg["S"])
+    flops = wl.flops("fwdbwd")
+    ksum = sum(kt.values())
+    del q, k, v, do
+    return {"workload": f"{name} on one GPU of {parts} (KV-group shard): B={cfg['B']} Hq={cfg['Hq']} "
+                        f"Hkv={cfg['Hkv']} L={cfg['L']} D={cfg['D']} W={cfg['W']} S={cfg['S']} {cfg['dtype']}, "
+                        f"fwd+bwd", "kernel_us": {n: round(x, 2) for n, x in kt.items()},
+            "kernel_sum_us": round(ksum, 2), "value": round(flops / (ksum * 1e-6) / 1e12, 2), "unit": "TFLOP/s",
+            "autograd_step_ms": round(t["fwdbwd_ms"], 4)}
+
+
 FP8_CONFIGS = ("c3", "c5", "c2")
 
 
@@ -502,6 +531,9 @@ def main():
     }
     if args.config == "c2" and not args.no_extras:
         line["varlen"] = varlen_measure(args.steps, args.warmup)
+        line["shard_proxy"] = sp = shard_proxy_measure(args.steps, args.warmup)
+        full = fb_flops / (sum(kt["avg_us"] for kt in line["kernels"].values()) * 1e-6) / 1e12
+        sp["per_gpu_vs_full"] = round(sp["value"] / full, 3)  # device throughput, share vs full shape
         line["fp8_forward"] = fp8_forward_measure()
     if not args.no_sdpa_baseline:
         line["sdpa_baseline"] = sdpa_baseline(cfg, q, k, v, do)
