@@ -196,6 +196,15 @@ def time_steps(fa, cfg, q, k, v, do, steps, warmup):
     torch.cuda.synchronize()
     fb_ms = (time.perf_counter() - t0) * 1e3 / steps
     fb_event_ms = ev0.elapsed_time(ev1) / steps
+    # per-step durations (an event before every step and after the last), for the median
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    for i in range(steps):
+        evs[i].record()
+        step()
+    evs[steps].record()
+    torch.cuda.synchronize()
+    per_step = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
+    fb_median_ms = per_step[steps // 2]
     peak_gb = torch.cuda.max_memory_allocated() / 2 ** 30
 
     # forward only (no autograd graph)
@@ -221,7 +230,8 @@ def time_steps(fa, cfg, q, k, v, do, steps, warmup):
         if i >= warmup:
             total += time.perf_counter() - t0
     b_ms = total * 1e3 / steps
-    return dict(fwdbwd_ms=fb_ms, fwdbwd_event_ms=fb_event_ms, fwd_ms=f_ms, bwd_ms=b_ms, peak_mem_gb=peak_gb)
+    return dict(fwdbwd_ms=fb_ms, fwdbwd_event_ms=fb_event_ms, fwdbwd_median_ms=fb_median_ms, fwd_ms=f_ms,
+                bwd_ms=b_ms, peak_mem_gb=peak_gb)
 
 
 VARLEN_SEQS = (4096, 2048, 1024, 512, 3000, 1500, 700, 3504)  # 16384 packed rows
@@ -383,10 +393,11 @@ def sdpa_baseline(cfg, q, k, v, do, steps=10, warmup=3):
             "steps": steps, "dtype": cfg["dtype"]}
 
 
-def cpu_baseline(cfg, budget_s):
+def cpu_baseline(cfg, budget_s, fp32=False):
     """The reference's naive path (benchmark_backward_speed.py:68-85, restated in oracle/naive.py)
-    in the config dtype on the host cores, forward + autograd backward, on whole KV groups of the
-    same workload until `budget_s` seconds have been spent (at least one group)."""
+    in the config dtype (fp32 with `fp32`, on the same values) on the host cores, forward +
+    autograd backward, on whole KV groups of the same workload until `budget_s` seconds have been
+    spent (at least one group)."""
     import torch
 
     from oracle import naive  # the CPU baseline leg
@@ -397,6 +408,9 @@ def cpu_baseline(cfg, budget_s):
     B, Hq, Hkv, L, D, W, S = (cfg[x] for x in ("B", "Hq", "Hkv", "L", "D", "W", "S"))
     G = Hq // Hkv
     q, k, v, do = make_inputs(cfg, "cpu")
+    if fp32:
+        q, k, v, do = (x.float() for x in (q, k, v, do))
+    dname = "fp32" if fp32 else cfg["dtype"]
     # warm up the thread pool and allocator on one head of a short prefix
     qw = q[:1, :1, :256].clone().requires_grad_()
     ow = naive.naive_attention(qw, k[:1, :1, :256], v[:1, :1, :256], W, S)
@@ -432,7 +446,7 @@ def cpu_baseline(cfg, budget_s):
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"{groups} KV-group passes ({passes} full passes over the {total_groups} KV groups of the same "
-                  f"workload, {groups * G} query-head passes), fwd+bwd of the naive path in {cfg['dtype']} (dense "
+                  f"workload, {groups * G} query-head passes), fwd+bwd of the naive path in {dname} (dense "
                   f"scores, fp32 softmax, autograd), {elapsed:.1f} s; full-workload estimate "
                   f"{elapsed * total_groups / groups * 1e3:.0f} ms",
         "ms_full_workload_est": elapsed * total_groups / groups * 1e3,
@@ -524,6 +538,7 @@ def main():
         "fwd_ms": round(t["fwd_ms"], 4),
         "bwd_ms": round(t["bwd_ms"], 4),
         "fwdbwd_event_ms": round(t["fwdbwd_event_ms"], 4),
+        "fwdbwd_median_ms": round(t["fwdbwd_median_ms"], 4),
         "peak_mem_gb": round(t["peak_mem_gb"], 4),
         "fwdbwd_roofline_frac": round(wl.roofline_seconds("fwdbwd") / (t["fwdbwd_ms"] * 1e-3), 4),
         "kernels": kernels,
@@ -539,6 +554,9 @@ def main():
         line["sdpa_baseline"] = sdpa_baseline(cfg, q, k, v, do)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_baseline_seconds)
+        # the same path in fp32 (the reference times the config dtype; fp32 is reported beside it)
+        f32 = cpu_baseline(cfg, args.cpu_baseline_seconds / 2, fp32=True)
+        line["cpu_baseline"]["fp32"] = {k: f32[k] for k in ("value", "unit", "sample", "ms_full_workload_est")}
     if args.table:
         for name, c in CONFIGS.items():
             qq, kk, vv, dd = make_inputs(c, dev)
