@@ -959,6 +959,17 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
   fold_sink_key<E, D>(b, kvh, key, sq, part);
 }
 
+// The D = 128 dQ and dK/dV kernels are instantiated in fa_bwd_wide.hip, which includes this file
+// with FA_BWD_WIDE_TU defined and is compiled with another machine scheduler; everything below
+// belongs to this translation unit only.
+#ifndef FA_BWD_WIDE_TU
+extern template __global__ void bwd_dq_kernel<BF16, 128, false>(const Args);
+extern template __global__ void bwd_dq_kernel<BF16, 128, true>(const Args);
+extern template __global__ void bwd_dq_kernel<F16, 128, false>(const Args);
+extern template __global__ void bwd_dq_kernel<F16, 128, true>(const Args);
+extern template __global__ void bwd_dkdv_kernel<BF16, 128>(const Args);
+extern template __global__ void bwd_dkdv_kernel<F16, 128>(const Args);
+
 // ---------------------------------------------------------------------------------------------
 // Gradient of the learned sink logits: dsink[h] = sum over (b, 32-row block) of the dQ kernel's
 // partials, in a fixed order (each thread strides over the partials in order, then the waves'
@@ -1062,5 +1073,7 @@ hipError_t launch_bwd_sink_logits(const Args& a, hipStream_t s) {
   hipLaunchKernelGGL(bwd_sink_logit_kernel, dim3(a.Hq), dim3(256), 0, s, a);
   return hipGetLastError();
 }
+#endif  // FA_BWD_WIDE_TU
+
 
 }  // namespace fa
