@@ -959,10 +959,13 @@ __global__ __launch_bounds__(256) void bwd_sink_fold_kernel(const Args a) {
   fold_sink_key<E, D>(b, kvh, key, sq, part);
 }
 
-// The D = 128 dQ and dK/dV kernels are instantiated in fa_bwd_wide.hip, which includes this file
+// The D = 128 dQ and dK/dV kernels and the D = 64 dQ kernel without sink rows are instantiated in
+// fa_bwd_wide.hip, which includes this file
 // with FA_BWD_WIDE_TU defined and is compiled with another machine scheduler; everything below
 // belongs to this translation unit only.
 #ifndef FA_BWD_WIDE_TU
+extern template __global__ void bwd_dq_kernel<BF16, 64, false>(const Args);
+extern template __global__ void bwd_dq_kernel<F16, 64, false>(const Args);
 extern template __global__ void bwd_dq_kernel<BF16, 128, false>(const Args);
 extern template __global__ void bwd_dq_kernel<BF16, 128, true>(const Args);
 extern template __global__ void bwd_dq_kernel<F16, 128, false>(const Args);
