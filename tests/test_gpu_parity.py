@@ -146,7 +146,7 @@ def test_edge_cases(gpu, B, Hq, Hkv, L, D, W, S, dtype):
     run_case(B, Hq, Hkv, L, D, W, S, dtype, seed=L + D + W)
 
 
-def _random_cases(n=24, seed=2026):
+def _random_cases(n=40, seed=2026):
     """Shapes drawn from a fixed seed, for combinations the hand-picked cases above do not name:
     batch 1-3, KV heads 1-4, group sizes 1-8, lengths 1-900 (some not multiples of 32), every
     head dim, windows from 1 to past L, 0-80 positional sinks, both dtypes, scales around
