@@ -102,7 +102,7 @@ def test_learned_sinks_parity(gpu, B, Hq, Hkv, L, D, W, S, dtype):
     run_sinks_case(B, Hq, Hkv, L, D, W, S, dtype, seed=L + D)
 
 
-def _random_sink_cases(n=10, seed=4242):
+def _random_sink_cases(n=16, seed=4242):
     """Learned sink logits on shapes drawn from a fixed seed: every head dim, groups 1-8, lengths
     1-600, windows from 1 to past L with and without positional sinks, logits of scale 0.5-8."""
     import random
