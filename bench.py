@@ -101,21 +101,29 @@ STAGE_KERNELS = {"fwd": ["fwd_kernel"], "bwd_dq": ["bwd_dq_kernel"],
 
 
 def measured_traffic(config, stage):
-    """HBM bytes per launch of a stage, from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed
-    as profiles/<config>_hbm_traffic.txt (copy-calibrated); None when there is no summary."""
-    path = os.path.join(ROOT, "profiles", f"{config}_hbm_traffic.txt")
+    """(HBM bytes per launch of a stage, where the figure comes from).  Hardware counters cannot be
+    read inside this run, so the figure is the one in the rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    committed as profiles/<config>_hbm_traffic.txt (copy-calibrated), identified by the file's
+    sha256 prefix: it goes stale when a kernel changes and the profile is not regenerated.
+    (None, None) when there is no summary."""
+    import hashlib
+
+    rel = os.path.join("profiles", f"{config}_hbm_traffic.txt")
+    path = os.path.join(ROOT, rel)
     if not os.path.exists(path):
-        return None
+        return None, None
     rows = {}
-    with open(path) as f:
-        for line in f:
-            parts = line.split()
-            if len(parts) == 4 and parts[0].endswith("_kernel") and parts[3].isdigit():
-                rows[parts[0]] = int(parts[3])
+    with open(path, "rb") as f:
+        data = f.read()
+    for line in data.decode().splitlines():
+        parts = line.split()
+        if len(parts) == 4 and parts[0].endswith("_kernel") and parts[3].isdigit():
+            rows[parts[0]] = int(parts[3])
     names = STAGE_KERNELS[stage]
     if names[0] not in rows:
-        return None
-    return float(sum(rows.get(n, 0) for n in names))
+        return None, None
+    src = f"{rel} (committed rocprofv3 --pmc summary, sha256 {hashlib.sha256(data).hexdigest()[:12]})"
+    return float(sum(rows.get(n, 0) for n in names)), src
 
 
 def time_kernels(cfg, q, k, v, do, iters=50):
@@ -393,66 +401,106 @@ def sdpa_baseline(cfg, q, k, v, do, steps=10, warmup=3):
             "steps": steps, "dtype": cfg["dtype"]}
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), else what platform reports."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(cfg, budget_s, fp32=False):
     """The reference's naive path (benchmark_backward_speed.py:68-85, restated in oracle/naive.py)
-    in the config dtype (fp32 with `fp32`, on the same values) on the host cores, forward +
-    autograd backward, on whole KV groups of the same workload until `budget_s` seconds have been
-    spent (at least one group)."""
+    on the host cores, in the config dtype (fp32 with `fp32`, on the same values), timed as the
+    reference times its modes (benchmark_backward_speed.py:720-783): forward only (no autograd
+    graph), forward + backward, and backward only (a forward, then backward() timed alone); one
+    warm-up and three timed iterations per mode, median.  An iteration runs the naive path over a
+    sample of whole KV groups of the same workload (every query head of a group with its K/V
+    head), sized from the warm-up so that the whole measurement takes about `budget_s` seconds;
+    times are scaled by (all KV groups / sample groups) to the full workload, and labelled so.
+    Host memory: the rise of the process's peak resident set during the measurement."""
+    import resource
+
     import torch
 
     from oracle import naive  # the CPU baseline leg
 
     flops_mod = _mod("flops")
     torch.set_num_threads(len(os.sched_getaffinity(0)))
-    dt = {"bf16": torch.bfloat16, "fp16": torch.float16}[cfg["dtype"]]
     B, Hq, Hkv, L, D, W, S = (cfg[x] for x in ("B", "Hq", "Hkv", "L", "D", "W", "S"))
     G = Hq // Hkv
     q, k, v, do = make_inputs(cfg, "cpu")
     if fp32:
         q, k, v, do = (x.float() for x in (q, k, v, do))
     dname = "fp32" if fp32 else cfg["dtype"]
-    # warm up the thread pool and allocator on one head of a short prefix
-    qw = q[:1, :1, :256].clone().requires_grad_()
-    ow = naive.naive_attention(qw, k[:1, :1, :256], v[:1, :1, :256], W, S)
-    ow.backward(do[:1, :1, :256])
-    # whole passes over every KV group while the budget lasts (at least one group); a pass that
-    # the budget cuts short still counts its finished groups
-    groups = 0
-    passes = 0
-    t0 = time.perf_counter()
-    elapsed = 0.0
-    while elapsed < budget_s:
-        for b in range(B):
-            for g in range(Hkv):
-                qs = q[b:b + 1, g * G:(g + 1) * G].clone().requires_grad_()
-                ks = k[b:b + 1, g:g + 1].clone().requires_grad_()
-                vs = v[b:b + 1, g:g + 1].clone().requires_grad_()
-                o = naive.naive_attention(qs, ks, vs, W, S)
-                o.backward(do[b:b + 1, g * G:(g + 1) * G])
-                groups += 1
-                elapsed = time.perf_counter() - t0
-                if elapsed >= budget_s:
-                    break
-            if elapsed >= budget_s:
-                break
-        else:
-            passes += 1
+    rss0 = resource.getrusage(resource.RUSAGE_SELF).ru_maxrss  # KiB
+    all_groups = [(b, g) for g in range(Hkv) for b in range(B)]
+
+    def slices(groups):
+        return [(q[b:b + 1, g * G:(g + 1) * G], k[b:b + 1, g:g + 1], v[b:b + 1, g:g + 1], do[b:b + 1, g * G:(g + 1) * G])
+                for b, g in groups]
+
+    def fwd(groups):
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            for qs, ks, vs, _ in slices(groups):
+                naive.naive_attention(qs, ks, vs, W, S)
+        return time.perf_counter() - t0
+
+    def fwdbwd(groups):
+        t0 = time.perf_counter()
+        for qs, ks, vs, ds in slices(groups):
+            qg, kg, vg = (x.clone().requires_grad_() for x in (qs, ks, vs))
+            naive.naive_attention(qg, kg, vg, W, S).backward(ds)
+        return time.perf_counter() - t0
+
+    def bwd(groups):
+        total = 0.0
+        for qs, ks, vs, ds in slices(groups):
+            qg, kg, vg = (x.clone().requires_grad_() for x in (qs, ks, vs))
+            o = naive.naive_attention(qg, kg, vg, W, S)
+            t0 = time.perf_counter()
+            o.backward(ds)
+            total += time.perf_counter() - t0
+        return total
+
+    # warm-up on one group; it also sizes the sample (a mode's 3 iterations plus the others'
+    # take about 8 fwd+bwd passes of the sample)
+    t_one = fwdbwd(all_groups[:1])
+    n = max(1, min(len(all_groups), int(budget_s / (8.0 * max(t_one, 1e-3)))))
+    sample = all_groups[:n]
+    modes = {}
+    for name, fn in (("fwd", fwd), ("fwdbwd", fwdbwd), ("bwd", bwd)):
+        fn(sample[:1])  # warm-up
+        ts = sorted(fn(sample) for _ in range(3))
+        modes[name] = ts[1] * len(all_groups) / n * 1e3  # median, scaled to the full workload (ms)
+    rss1 = resource.getrusage(resource.RUSAGE_SELF).ru_maxrss
     pairs = flops_mod.allowed_pairs_per_head(L, W, S)
-    flops = 14.0 * D * pairs * groups * G
-    total_groups = B * Hkv
+    flops = 14.0 * D * pairs * B * Hq
+    scaled = n < len(all_groups)
     return {
-        "value": flops / elapsed / 1e12,
+        "value": flops / (modes["fwdbwd"] * 1e-3) / 1e12,
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{groups} KV-group passes ({passes} full passes over the {total_groups} KV groups of the same "
-                  f"workload, {groups * G} query-head passes), fwd+bwd of the naive path in {dname} (dense "
-                  f"scores, fp32 softmax, autograd), {elapsed:.1f} s; full-workload estimate "
-                  f"{elapsed * total_groups / groups * 1e3:.0f} ms",
-        "ms_full_workload_est": elapsed * total_groups / groups * 1e3,
-        "cpu": platform.processor() or platform.machine(),
+        "sample": f"{n} of the {len(all_groups)} KV groups of the workload ({n * G} query heads) per iteration, "
+                  f"naive path in {dname} (dense scores, fp32 softmax, autograd backward), warm-up 1 + median of 3 "
+                  f"per mode; times {'scaled x' + format(len(all_groups) / n, '.3g') + ' to the full workload (extrapolated)' if scaled else 'of the full workload'}",
+        "fwd_ms": round(modes["fwd"], 2),
+        "fwdbwd_ms": round(modes["fwdbwd"], 2),
+        "bwd_ms": round(modes["bwd"], 2),
+        "ms_full_workload_est": modes["fwdbwd"],
+        "extrapolated": scaled,
+        "max_rss_delta_mb": round((rss1 - rss0) / 1024.0, 1),
+        "cpu": cpu_model(),
         "logical_cores": os.cpu_count(),
         "torch_threads": torch.get_num_threads(),
+        "torch": torch.__version__,
+        "dtype": dname,
     }
 
 
@@ -497,8 +545,11 @@ def main():
     acct = kernel_accounting(cfg)
     wl = _mod("flops").Workload(cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"], cfg["D"], cfg["W"], cfg["S"])
 
-    t = time_steps(fa, cfg, q, k, v, do, args.steps, args.warmup)
+    # The per-kernel timing runs first: its few hundred launches also bring the GPU's clocks to
+    # their working level before the warm-up and timed steps (with only a handful of warm-up
+    # steps on a cold GPU, the timed steps would otherwise run partly at idle clocks).
     kus = time_kernels(cfg, q, k, v, do, iters=args.kernel_iters)
+    t = time_steps(fa, cfg, q, k, v, do, args.steps, args.warmup)
 
     kernels = {}
     for name, us in kus.items():
@@ -513,9 +564,20 @@ def main():
         achieved, peak, unit = dk["gbs"], HBM_PEAK_GBS, "GB/s"
     else:
         achieved, peak, unit = dk["tflops"], MFMA_PEAK_TFLOPS, "TFLOP/s"
+    traffic, traffic_src = measured_traffic(args.config, dom)
+    # the backward as one unit (the survey's figure: each tensor read or written once, delta fused):
+    # its algorithmic bytes or FLOPs over the two backward kernels' summed time
+    bwd_us = kernels["bwd_dq"]["avg_us"] + kernels["bwd_dkdv"]["avg_us"]
+    bwd_bound = "hbm" if wl.flops("bwd") / wl.bytes("bwd") < MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma"
+    bwd_ach = (wl.bytes("bwd") / bwd_us / 1e3) if bwd_bound == "hbm" else (wl.flops("bwd") / bwd_us / 1e6)
     roofline = {"kernel": dom, "bound": dk["bound"], "achieved": achieved, "peak": peak, "unit": unit,
-                "frac": round(achieved / peak, 4), "traffic": measured_traffic(args.config, dom),
-                "avg_us": dk["avg_us"], "alg_bytes": dk["alg_bytes"]}
+                "frac": round(achieved / peak, 4), "traffic": traffic, "traffic_source": traffic_src,
+                "avg_us": dk["avg_us"], "alg_bytes": dk["alg_bytes"],
+                "fused_backward": {"kernels": ["bwd_dq", "bwd_dkdv"], "us": round(bwd_us, 3), "bound": bwd_bound,
+                                   "alg_bytes": wl.bytes("bwd"), "useful_flops": wl.flops("bwd"),
+                                   "achieved": round(bwd_ach, 1),
+                                   "unit": "GB/s" if bwd_bound == "hbm" else "TFLOP/s",
+                                   "frac": round(bwd_ach / (HBM_PEAK_GBS if bwd_bound == "hbm" else MFMA_PEAK_TFLOPS), 4)}}
 
     fb_flops = wl.flops("fwdbwd")
     value = fb_flops / (t["fwdbwd_ms"] * 1e-3) / 1e12
@@ -556,7 +618,8 @@ def main():
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_baseline_seconds)
         # the same path in fp32 (the reference times the config dtype; fp32 is reported beside it)
         f32 = cpu_baseline(cfg, args.cpu_baseline_seconds / 2, fp32=True)
-        line["cpu_baseline"]["fp32"] = {k: f32[k] for k in ("value", "unit", "sample", "ms_full_workload_est")}
+        line["cpu_baseline"]["fp32"] = {k: f32[k] for k in ("value", "unit", "sample", "fwd_ms", "fwdbwd_ms", "bwd_ms",
+                                                            "extrapolated", "max_rss_delta_mb")}
     if args.table:
         for name, c in CONFIGS.items():
             qq, kk, vv, dd = make_inputs(c, dev)

@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes
 import importlib
+import warnings
 
 import torch
 
@@ -143,11 +144,14 @@ def _binding():
     C ABI of libfa_gfx950.so; the binding only does the per-call host work in C++."""
     global _BINDING
     if _BINDING is False:
+        _lib.lib()  # the HIP library is required either way (raises when missing)
         try:
-            _lib.lib()  # the HIP library is required either way (raises when missing)
             _BINDING = importlib.import_module(__package__ + ".fa_torch")
-        except ImportError:
+        except ImportError as e:
             _BINDING = None
+            warnings.warn(f"the C++ PyTorch binding fa_torch could not be imported ({e}); the attention calls go "
+                          "through ctypes instead, which costs about 100 us of host time per forward + backward "
+                          "(build it with csrc/build_torch_ext.py)", RuntimeWarning, stacklevel=3)
     return _BINDING
 
 
@@ -308,6 +312,16 @@ def backward(q, k, v, o, lse, do, window: int, sink: int, scale: float, sinks=No
     if sinks is None:
         return call.dq, call.dk, call.dv
     return call.dq, call.dk, call.dv, call.dsinks
+
+
+def backward_staged(q, k, v, o, lse, do, window: int, sink: int, scale: float):
+    """(dq, dk, dv) through the two stages of the backward as separate C-ABI calls on one
+    workspace: fa_bwd_dq (dq and the row statistic delta) then fa_bwd_dkdv (dk and dv), the
+    benchmark's split backward (benchmark_backward_speed.py:574-612)."""
+    call = BwdCall(q, k, v, o, lse, do, window, sink, scale)
+    call.run("dq")
+    call.run("dkdv")
+    return call.dq, call.dk, call.dv
 
 
 # ---- variable-length batches ------------------------------------------------------------------

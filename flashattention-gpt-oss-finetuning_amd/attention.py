@@ -187,5 +187,39 @@ def flash_swda_with_sink(q, k, v, window_size: int, sink_size: int = 0, is_causa
 
 def swa_sink_attention(q, k, v, window_size: int, sink_size: int):
     """Registry form ``func(q, k, v, window_size, sink_size) -> o`` with the default scale 1/sqrt(D)
-    (benchmark_backward_speed.py:615-643)."""
+    (triton_attention, benchmark_backward_speed.py:615-622): one backward call, fa_bwd."""
     return FlashSWDAWithSink.apply(q, k, v, window_size, sink_size, True, None)
+
+
+class FlashSWDAWithSinkSplit(torch.autograd.Function):
+    """The benchmark's split-backward variant (TritonSWASinkAttentionSplit,
+    benchmark_backward_speed.py:533-612): the same forward, and a backward made of two separate
+    launches on one workspace -- fa_bwd_dq (dQ and the row statistic delta), then fa_bwd_dkdv
+    (dK and dV).  Results equal FlashSWDAWithSink's bit for bit.
+
+    forward(q, k, v, window_size, sink_size, softmax_scale=None) -> o; backward returns 6 values."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, window_size, sink_size, softmax_scale=None):
+        if softmax_scale is None:
+            softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+        _check_shapes(q, k, v)
+        o, lse = _ops.forward(q, k, v, int(window_size), int(sink_size), float(softmax_scale))
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.softmax_scale = softmax_scale
+        ctx.window_size = window_size
+        ctx.sink_size = sink_size
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = _ops.backward_staged(q, k, v, o, lse, do, int(ctx.window_size), int(ctx.sink_size),
+                                          float(ctx.softmax_scale))
+        return dq, dk, dv, None, None, None
+
+
+def swa_sink_attention_split(q, k, v, window_size: int, sink_size: int):
+    """Registry form of the split-backward variant (triton_attention_split,
+    benchmark_backward_speed.py:625-632)."""
+    return FlashSWDAWithSinkSplit.apply(q, k, v, window_size, sink_size, None)

@@ -102,6 +102,19 @@ using KArgs = const Args;
 __device__ KArgs& args_fresh();  // device code only
 #endif
 
+// Rows of a packed (variable-length) batch that belong to no sequence -- [0, cu_seqlens[0]) and
+// [cu_seqlens[B], total_rows) -- are written by no attention kernel.  varlen_tail_kernel fills
+// them in up to three outputs: every (row, head) of tensor i gets `cols[i]` elements of
+// `elem_bytes[i]` bytes (2 or 4) set to the bit pattern `fill[i]`.  Strides are in elements.
+struct TailArgs {
+  const int* cu_seqlens;
+  int batch, total_rows, n;
+  void* ptr[3];
+  int64_t head_stride[3], row_stride[3];
+  int heads[3], cols[3], elem_bytes[3];
+  uint32_t fill[3];
+};
+
 // Launchers (return the hipError_t of the launch; launch_bwd_dkdv also launches the sink fold).
 hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
 // e4m3 q, k, v; bf16 o; fp8_pv: P V on the fp8 MFMA as well
@@ -109,5 +122,6 @@ hipError_t launch_fwd_fp8(const Args& a, int D, int hpw, bool fp8_pv, hipStream_
 hipError_t launch_bwd_dq(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
 hipError_t launch_bwd_dkdv(const Args& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_bwd_sink_logits(const Args& a, hipStream_t stream);  // after launch_bwd_dq
+hipError_t launch_varlen_tail(const TailArgs& t, hipStream_t stream);
 
 }  // namespace fa

@@ -996,6 +996,41 @@ __global__ __launch_bounds__(256) void bwd_sink_logit_kernel(const Args a) {
   if (tid == 0) a.dsink[h] = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Packed rows outside every sequence (see TailArgs): one thread per (row, head) of each tensor, in
+// a grid-stride loop over the uncovered rows.  With cu_seqlens[0] = 0 and cu_seqlens[B] =
+// total_rows (the usual case) every workgroup reads two offsets and exits.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void varlen_tail_kernel(const TailArgs t) {
+  const int total = t.total_rows;
+  int lo = t.cu_seqlens[0], hi = t.cu_seqlens[t.batch];
+  lo = lo < 0 ? 0 : (lo > total ? total : lo);
+  hi = hi < lo ? lo : (hi > total ? total : hi);
+  const int64_t n_rows = int64_t(lo) + (total - hi);  // uncovered rows, [0, lo) then [hi, total)
+  if (n_rows == 0) return;
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int i = 0; i < t.n; ++i) {
+    const int64_t units = n_rows * t.heads[i];
+    for (int64_t u = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; u < units; u += stride) {
+      const int64_t r = u / t.heads[i];
+      const int h = int(u % t.heads[i]);
+      const int64_t row = r < lo ? r : hi + (r - lo);
+      char* p = static_cast<char*>(t.ptr[i]) + (h * t.head_stride[i] + row * t.row_stride[i]) * t.elem_bytes[i];
+      if (t.elem_bytes[i] == 4) {
+        for (int c = 0; c < t.cols[i]; ++c) reinterpret_cast<uint32_t*>(p)[c] = t.fill[i];
+      } else {
+        const uint32_t f2 = (t.fill[i] & 0xffffu) * 0x10001u;
+        for (int c = 0; c < t.cols[i]; c += 8) st16(p + 2 * c, u32x4{f2, f2, f2, f2});  // rows 16-byte aligned
+      }
+    }
+  }
+}
+
+hipError_t launch_varlen_tail(const TailArgs& t, hipStream_t stream) {
+  hipLaunchKernelGGL(varlen_tail_kernel, dim3(256), dim3(256), 0, stream, t);
+  return hipGetLastError();
+}
+
 // Resident workgroups per CU of a kernel (hipOccupancyMaxActiveBlocksPerMultiprocessor,
 // 256 threads), remembered per kernel (one cache per template argument, i.e. per kernel): it
 // depends only on the kernel's resources.

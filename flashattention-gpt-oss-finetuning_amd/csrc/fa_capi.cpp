@@ -160,8 +160,11 @@ int fa_check_fwd(const fa_fwd_params* p) {
   if (!strides_ok(p->q_stride) || !strides_ok(p->k_stride) || !strides_ok(p->v_stride) ||
       !strides_ok(p->o_stride) || !lse_strides_ok(p->lse_stride))
     return FA_ERR_ALIGN;
+  // q, k and v are staged through buffer resources with 32-bit byte offsets inside one
+  // (batch, head) slice; o and lse are written through 64-bit addresses
   const int L = p->seqlen, D = p->head_dim;
-  if (!slice_fits(p->k_stride, L, D, 2) || !slice_fits(p->v_stride, L, D, 2)) return FA_ERR_OVERFLOW;
+  if (!slice_fits(p->q_stride, L, D, 2) || !slice_fits(p->k_stride, L, D, 2) || !slice_fits(p->v_stride, L, D, 2))
+    return FA_ERR_OVERFLOW;
   return FA_OK;
 }
 
@@ -180,9 +183,11 @@ int fa_check_bwd(const fa_bwd_params* p) {
       !strides_ok(p->o_stride) || !strides_ok(p->do_stride) || !lse_strides_ok(p->lse_stride) ||
       !strides_ok(p->dq_stride) || !strides_ok(p->dk_stride) || !strides_ok(p->dv_stride))
     return FA_ERR_ALIGN;
+  // every input is read through buffer resources with 32-bit byte offsets inside one
+  // (batch, head) slice; dq, dk and dv are written through 64-bit addresses
   const int L = p->seqlen, D = p->head_dim;
-  if (!slice_fits(p->q_stride, L, D, 2) || !slice_fits(p->do_stride, L, D, 2) || !slice_fits(p->lse_stride, L, 1, 4) ||
-      !slice_fits(p->k_stride, L, D, 2) || !slice_fits(p->v_stride, L, D, 2))
+  if (!slice_fits(p->q_stride, L, D, 2) || !slice_fits(p->do_stride, L, D, 2) || !slice_fits(p->o_stride, L, D, 2) ||
+      !slice_fits(p->lse_stride, L, 1, 4) || !slice_fits(p->k_stride, L, D, 2) || !slice_fits(p->v_stride, L, D, 2))
     return FA_ERR_OVERFLOW;
   return FA_OK;
 }
@@ -197,6 +202,28 @@ int check_varlen(const int32_t* cu_seqlens, int32_t total_rows) {
   if (!aligned4(cu_seqlens)) return FA_ERR_ALIGN;
   if (total_rows < 0) return FA_ERR_SHAPE;
   return FA_OK;
+}
+
+// Adds tensor (ptr, strides s = batch/head/row, heads, cols, element bytes, fill bits) to the
+// outputs whose uncovered packed rows varlen_tail_kernel fills.
+void tail_add(fa::TailArgs* t, void* ptr, const int64_t s[3], int heads, int cols, int eb, uint32_t fill) {
+  const int i = t->n++;
+  t->ptr[i] = ptr;
+  t->head_stride[i] = s[1];
+  t->row_stride[i] = s[2];
+  t->heads[i] = heads;
+  t->cols[i] = cols;
+  t->elem_bytes[i] = eb;
+  t->fill[i] = fill;
+}
+
+fa::TailArgs tail_args(const int32_t* cu_seqlens, int32_t batch, int32_t total_rows) {
+  fa::TailArgs t;
+  std::memset(&t, 0, sizeof(t));
+  t.cu_seqlens = cu_seqlens;
+  t.batch = batch;
+  t.total_rows = total_rows;
+  return t;
 }
 
 void set_varlen(fa::Args* a, const int32_t* cu_seqlens, int32_t total_rows) {
@@ -295,7 +322,13 @@ int fa_fwd_varlen(const fa_fwd_params* p, const int32_t* cu_seqlens, int32_t tot
   if (rc == FA_OK) rc = check_varlen(cu_seqlens, total_rows);
   if (rc != FA_OK) return rc;
   if (sinks && !aligned4(sinks)) return FA_ERR_ALIGN;
-  return run_fwd(p, sinks, stream, cu_seqlens, total_rows);
+  rc = run_fwd(p, sinks, stream, cu_seqlens, total_rows);
+  if (rc != FA_OK) return rc;
+  // rows outside every sequence: o = 0, lse = -inf (an empty row)
+  fa::TailArgs t = tail_args(cu_seqlens, p->batch, total_rows);
+  tail_add(&t, p->o, p->o_stride, p->heads_q, p->head_dim, 2, 0u);
+  tail_add(&t, p->lse, p->lse_stride, p->heads_q, 1, 4, 0xff800000u);
+  return fa::launch_varlen_tail(t, static_cast<hipStream_t>(stream)) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 
 int fa_fwd_fp8(const fa_fwd_params* p, float q_descale, float k_descale, float v_descale, const float* sinks,
@@ -442,7 +475,14 @@ int fa_bwd_varlen(const fa_bwd_params* p, const int32_t* cu_seqlens, int32_t tot
   const hipStream_t s = static_cast<hipStream_t>(stream);
   int r = run_dq(a, p, hpw, s);
   if (r == FA_OK && sinks) r = fa::launch_bwd_sink_logits(a, s) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
-  return r != FA_OK ? r : run_dkdv(a, p, s);
+  if (r == FA_OK) r = run_dkdv(a, p, s);
+  if (r != FA_OK) return r;
+  // rows outside every sequence have zero gradients
+  fa::TailArgs t = tail_args(cu_seqlens, p->batch, total_rows);
+  tail_add(&t, p->dq, p->dq_stride, p->heads_q, p->head_dim, 2, 0u);
+  tail_add(&t, p->dk, p->dk_stride, p->heads_kv, p->head_dim, 2, 0u);
+  tail_add(&t, p->dv, p->dv_stride, p->heads_kv, p->head_dim, 2, 0u);
+  return fa::launch_varlen_tail(t, s) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 
 int fa_bwd_dq(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream) {

@@ -16,11 +16,70 @@ read in place, and outputs take the inputs' memory layout, so neither layout is 
 """
 from __future__ import annotations
 
+import weakref
 from typing import Optional
 
 import torch
 
 from .attention import FlashSWDAWithLearnedSinks, FlashSWDAWithSink, flash_swda_with_sink_varlen
+
+
+class _BatchFacts:
+    """Host-side facts about one batch's padding mask or position ids (which rows hold tokens,
+    where the packed sequences start, the longest one).  Working them out reads device memory,
+    i.e. synchronises the host once; transformers hands the same tensor object to every attention
+    layer of a forward pass, so the facts are kept for that tensor (while it lives and is not
+    modified in place) and the other layers enqueue their kernels without waiting for the GPU."""
+
+    __slots__ = ("_ref", "_key", "_val")
+
+    def __init__(self):
+        self._ref = None
+        self._key = None
+        self._val = None
+
+    def get(self, t: torch.Tensor, compute):
+        key = (t.data_ptr(), t._version, tuple(t.shape), t.dtype, t.device)
+        if self._ref is not None and self._ref() is t and self._key == key:
+            return self._val
+        val = compute(t)
+        self._ref, self._key, self._val = weakref.ref(t), key, val
+        return val
+
+
+_MASK_FACTS = _BatchFacts()
+_POSITION_FACTS = _BatchFacts()
+_CU_FACTS = _BatchFacts()
+
+
+def _mask_facts(attention_mask: torch.Tensor):
+    """(all rows are tokens, token row indices of the [B * L] flattening, cu_seqlens int32 [B + 1],
+    longest sequence) of a [B, L] padding mask (nonzero = token)."""
+    m = attention_mask.to(dtype=torch.bool)
+    if bool(m.all()):
+        return True, None, None, m.shape[1]
+    B = m.shape[0]
+    idx = m.reshape(-1).nonzero().squeeze(1)
+    lens = m.sum(1, dtype=torch.int32)
+    cu = torch.zeros(B + 1, dtype=torch.int32, device=m.device)
+    cu[1:] = lens.cumsum(0)
+    return False, idx, cu, int(lens.max()) if B else 0
+
+
+def _position_facts(position_ids: torch.Tensor):
+    """(cu_seqlens int32 [n + 1], longest sequence) of a packed row of several sequences, or None.
+    As transformers' flash-attention path does (_is_packed_sequence,
+    prepare_fa_kwargs_from_position_ids): a single row whose position ids are not one increasing
+    run holds several sequences, each starting where the ids return to their minimum."""
+    if position_ids.dim() != 2 or position_ids.shape[0] != 1:
+        return None
+    p = position_ids.reshape(-1)
+    first = p.min()
+    if bool((p == torch.arange(p.numel(), device=p.device) + first).all()):
+        return None
+    starts = (p == first).nonzero().view(-1).to(torch.int32)
+    cu = torch.cat((starts, torch.tensor([p.numel()], dtype=torch.int32, device=p.device)))
+    return cu, int(cu.diff().max())
 
 
 def attention(q, k, v, window_size: Optional[int] = None, sink_size: int = 0, sinks: Optional[torch.Tensor] = None,
@@ -48,9 +107,14 @@ def gpt_oss_attention_forward(module, query, key, value, attention_mask, dropout
 
     Supported: training and prefill, no dropout.  attention_mask is None or the 2-D [B, L] padding
     mask that transformers' flash-attention mask function hands over (True or 1 = a token); a
-    padded batch runs as a packed variable-length batch (padded_attention).  KV caches (query
-    shorter than key), other mask forms and dropout raise NotImplementedError rather than
-    computing something else."""
+    padded batch runs as a packed variable-length batch (padded_attention).  Without a mask,
+    several sequences packed into one row (padding-free finetuning) are recognised as
+    transformers' flash-attention path recognises them: from the data collator's cu_seq_lens_q /
+    max_length_q keyword arguments, or from position_ids that restart inside the row; they run as
+    a packed batch too, so no token attends across a sequence boundary.  The host reads the mask
+    or the position ids once per batch (the first layer); the other layers reuse what it found.
+    KV caches (query shorter than key), other mask forms and dropout raise NotImplementedError
+    rather than computing something else."""
     if dropout:
         raise NotImplementedError("attention dropout is not implemented by the gfx950 kernels")
     if query.shape[2] != key.shape[2]:
@@ -59,16 +123,52 @@ def gpt_oss_attention_forward(module, query, key, value, attention_mask, dropout
         if attention_mask.dim() != 2:
             raise NotImplementedError("only the 2-D [batch, seq] padding mask of the flash-attention mask function "
                                       f"is supported, got a {attention_mask.dim()}-D mask")
-        if not bool(attention_mask.all()):
+        facts = _MASK_FACTS.get(attention_mask, lambda m: _mask_facts(m.to(query.device)))
+        if not facts[0]:
             o = padded_attention(query, key, value, attention_mask, window_size=sliding_window, sinks=s_aux,
-                                 scale=scaling)
+                                 scale=scaling, _facts=facts)
             return o, None
+    else:
+        packed = _packed_sequences(query, kwargs)
+        if packed is not None:
+            return _packed_row_attention(query, key, value, packed[0], packed[1], sliding_window, s_aux, scaling), None
     o = attention(query, key, value, window_size=sliding_window, sinks=s_aux, scale=scaling)
     return o.transpose(1, 2), None
 
 
+def _packed_sequences(query, kwargs):
+    """(cu_seqlens, longest sequence) when the unmasked batch packs several sequences per row,
+    else None: the collator's cu_seq_lens_q (with max_length_q), or restarting position_ids."""
+    cu_q = kwargs.get("cu_seq_lens_q")
+    if cu_q is not None:
+        cu_k = kwargs.get("cu_seq_lens_k")
+        if cu_k is not None and cu_k is not cu_q and not torch.equal(cu_k.to(cu_q.device), cu_q):
+            raise NotImplementedError("cu_seq_lens_k differs from cu_seq_lens_q; only self-attention over the same "
+                                      "packed sequences is supported")
+        max_len = kwargs.get("max_length_q")
+
+        def facts(cu):
+            n = int(cu.diff().max()) if max_len is None else int(max_len)
+            return cu.to(device=query.device, dtype=torch.int32), n
+        return _CU_FACTS.get(cu_q, facts)
+    position_ids = kwargs.get("position_ids")
+    if position_ids is None or query.shape[0] != 1:
+        return None
+    return _POSITION_FACTS.get(position_ids, lambda p: _position_facts(p.to(query.device)))
+
+
+def _packed_row_attention(q, k, v, cu, max_len, window_size, sinks, scale):
+    """Attention over B x L rows flattened into one packed batch with offsets cu (sequence b is
+    flattened rows [cu[b], cu[b + 1])).  Returns [B, L, Hq, D]."""
+    B, Hq, L, D = q.shape
+    flat = lambda x: x.transpose(1, 2).reshape(B * L, x.shape[1], D)
+    W = max_len if window_size is None else int(window_size)
+    o = flash_swda_with_sink_varlen(flat(q), flat(k), flat(v), cu, max_len, W, 0, scale, sinks)
+    return o.view(B, L, Hq, D)
+
+
 def padded_attention(q, k, v, attention_mask, window_size: Optional[int] = None, sinks: Optional[torch.Tensor] = None,
-                     scale: Optional[float] = None):
+                     scale: Optional[float] = None, _facts=None):
     """Attention over a padded batch: q [B, Hq, L, D], k/v [B, Hkv, L, D], attention_mask [B, L]
     (nonzero = token).  The tokens of each row are gathered, in order, into one packed batch with
     cu_seqlens and run through flash_swda_with_sink_varlen, so causality, the window and the sinks
@@ -78,12 +178,12 @@ def padded_attention(q, k, v, attention_mask, window_size: Optional[int] = None,
     B, Hq, L, D = q.shape
     if tuple(attention_mask.shape) != (B, L):
         raise ValueError(f"attention_mask must be [B, L] = [{B}, {L}], got {tuple(attention_mask.shape)}")
-    m = attention_mask.to(device=q.device, dtype=torch.bool)
-    idx = m.reshape(-1).nonzero().squeeze(1)  # token rows of the [B * L] flattening, in order
-    lens = m.sum(1, dtype=torch.int32)
-    cu = torch.zeros(B + 1, dtype=torch.int32, device=q.device)
-    cu[1:] = lens.cumsum(0)
-    max_len = int(lens.max()) if B else 0
+    if _facts is None:
+        _facts = _mask_facts(attention_mask.to(device=q.device))
+    # token rows of the [B * L] flattening (in order), their offsets, the longest sequence
+    _, idx, cu, max_len = _facts
+    if idx is None:  # every row is a token
+        return attention(q, k, v, window_size=window_size, sinks=sinks, scale=scale).transpose(1, 2)
     if max_len == 0:
         return q.new_zeros(B, L, Hq, D)
 

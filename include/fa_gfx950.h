@@ -168,6 +168,9 @@ int fa_bwd_sinks(const fa_bwd_params* p, const float* sinks, float* dsinks, void
  *     offsets cannot address memory outside the tensors; the results are then meaningless).
  *   - Causality, the window and the S positional sinks apply within each sequence: a row never
  *     sees another sequence's keys, and the sinks are each sequence's first S keys.
+ *   - Rows that belong to no sequence, [0, cu_seqlens[0]) and [cu_seqlens[batch], total_rows),
+ *     get o = 0 and lse = -inf from fa_fwd_varlen and zero dq, dk, dv from fa_bwd_varlen (one
+ *     small extra launch, which exits at once when every row is covered).
  *   - sinks (float32 [Hq]) may be NULL; fa_bwd_varlen takes sinks and dsinks together or
  *     neither.  The workspace is fa_bwd_workspace_bytes(batch, Hq, Hkv, p->seqlen, D, W, S). */
 int fa_fwd_varlen(const fa_fwd_params* p, const int32_t* cu_seqlens, int32_t total_rows, const float* sinks,

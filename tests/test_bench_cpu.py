@@ -51,3 +51,23 @@ def test_bench_measures_one_gpu_only():
                        cwd=bench.__file__.rsplit("/", 1)[0])
     assert r.returncode == 2
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+def test_cpu_baseline_reports_three_modes_on_a_small_workload():
+    """The CPU baseline leg runs on a small workload: forward, fwd+bwd and backward-only times,
+    the CPU model, cores and the host-memory rise are reported, and a sample smaller than the
+    workload is labelled as extrapolated."""
+    cfg = dict(B=1, Hq=4, Hkv=2, L=256, D=16, W=32, S=4, dtype="bf16", do_std=1.0, name="tiny")
+    r = bench.cpu_baseline(cfg, budget_s=0.5)
+    for k in ("fwd_ms", "fwdbwd_ms", "bwd_ms", "value", "cores", "cpu", "max_rss_delta_mb"):
+        assert k in r, k
+    assert r["fwd_ms"] > 0 and r["fwdbwd_ms"] > 0 and r["bwd_ms"] > 0
+    assert r["kind"] == "port" and r["unit"] == "TFLOP/s"
+    assert isinstance(r["extrapolated"], bool)
+    assert "extrapolated" in r["sample"] if r["extrapolated"] else "full workload" in r["sample"]
+
+
+def test_traffic_figure_names_its_source():
+    t, src = bench.measured_traffic("c2", "bwd_dq")
+    assert t is None or (t > 0 and "sha256" in src and "profiles/c2_hbm_traffic.txt" in src)
+    assert bench.measured_traffic("nonexistent", "fwd") == (None, None)

@@ -66,3 +66,25 @@ def test_gpt_oss_adapter_registers_with_transformers(fa):
     name = fa.register_transformers("fa_gfx950_test")
     assert AttentionInterface._global_mapping[name] is fa.gpt_oss_attention_forward
     assert name in ALL_MASK_ATTENTION_FUNCTIONS._global_mapping
+
+
+def test_missing_binding_warns_once(monkeypatch):
+    """Without the C++ binding the calls fall back to ctypes, which costs host time per step: the
+    fallback is announced with a RuntimeWarning (once), not taken silently."""
+    load_pkg()
+    ops = importlib.import_module("flashattention-gpt-oss-finetuning_amd._ops")
+    real = importlib.import_module
+
+    def no_binding(name, *a, **k):
+        if name.endswith(".fa_torch"):
+            raise ImportError("simulated: binding not built")
+        return real(name, *a, **k)
+
+    monkeypatch.setattr(ops, "_BINDING", False)
+    monkeypatch.setattr(ops.importlib, "import_module", no_binding)
+    with pytest.warns(RuntimeWarning, match="ctypes"):
+        assert ops._binding() is None
+    import warnings
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert ops._binding() is None  # cached: no second warning

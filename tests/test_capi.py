@@ -180,6 +180,32 @@ def test_check_rejects_kv_slices_beyond_32bit_offsets():
         assert L.fa_check_bwd(ctypes.byref(_bwd_params(seqlen=big, **{name: wide}))) == _lib.FA_ERR_OVERFLOW
 
 
+def test_check_rejects_q_and_o_slices_beyond_32bit_offsets():
+    """The forward stages q, and the dQ kernel stages q, dO and o, through buffer resources with
+    32-bit byte offsets inside one (batch, head) slice.  The [B, L, H, D] layout of a GPT-OSS
+    projection (sequence stride H * D) reaches 2^31 bytes per head slice at L = 300000 with
+    Hq = 64, D = 64: such a q or o is refused, not read through wrapped offsets."""
+    L = _lib.lib()
+    Lg, Hq, D = 300000, 64, 64
+    blhd = (Lg * Hq * D, D, Hq * D)  # [B, L, H, D] viewed as [B, H, L, D]
+    assert (Lg - 1) * Hq * D * 2 >= 1 << 31
+    fwd_ok = _fwd_params(seqlen=Lg)
+    assert L.fa_check_fwd(ctypes.byref(fwd_ok)) == _lib.FA_OK
+    assert L.fa_check_fwd(ctypes.byref(_fwd_params(seqlen=Lg, q_stride=blhd))) == _lib.FA_ERR_OVERFLOW
+    # o is written through 64-bit addresses by the forward: accepted there
+    assert L.fa_check_fwd(ctypes.byref(_fwd_params(seqlen=Lg, o_stride=blhd))) == _lib.FA_OK
+    for name in ("q_stride", "o_stride", "do_stride"):
+        assert L.fa_check_bwd(ctypes.byref(_bwd_params(seqlen=Lg, **{name: blhd}))) == _lib.FA_ERR_OVERFLOW, name
+    # the gradients are written through 64-bit addresses
+    for name in ("dq_stride", "dk_stride", "dv_stride"):
+        assert L.fa_check_bwd(ctypes.byref(_bwd_params(seqlen=Lg, **{name: blhd}))) == _lib.FA_OK, name
+    # the same shapes one row short of the limit are accepted: 2^31 / (Hq * D * 2) rows fit
+    Lok = (1 << 31) // (Hq * D * 2)
+    assert L.fa_check_fwd(ctypes.byref(_fwd_params(seqlen=Lok, q_stride=(Lok * Hq * D, D, Hq * D)))) == _lib.FA_OK
+    assert L.fa_check_fwd(ctypes.byref(_fwd_params(seqlen=Lok + 1, q_stride=(Lok * Hq * D, D, Hq * D)))) == \
+        _lib.FA_ERR_OVERFLOW
+
+
 def test_entry_points_reject_before_any_hip_call():
     """fa_fwd / fa_bwd return the validation code for bad arguments (this runs without a GPU)."""
     L = _lib.lib()

@@ -185,14 +185,14 @@ def test_custom_scales(gpu, scale):
     run_case(1, 4, 2, 200, 64, 48, 4, BF, seed=3, scale=scale)
 
 
-# BASELINE configs c1..c5 at full size.  Where a full float32 oracle pass over every head would
-# be slow, whole KV groups are checked (dK/dV need every query head of their group).
+# BASELINE configs c1..c5 at full size, every head and every KV group (the float32 oracle runs
+# on the GPU, 2048 query rows at a time).
 @pytest.mark.parametrize("cfg", [
     pytest.param(dict(B=1, Hq=16, Hkv=16, L=4096, D=16, W=256, S=4, dtype=FP), id="c1"),
     pytest.param(dict(B=1, Hq=64, Hkv=8, L=4096, D=64, W=128, S=4, dtype=BF), id="c2"),
-    pytest.param(dict(B=1, Hq=64, Hkv=8, L=8192, D=64, W=8192, S=0, dtype=BF, heads=list(range(8)) + list(range(56, 64))), id="c3"),
-    pytest.param(dict(B=1, Hq=64, Hkv=8, L=32768, D=64, W=128, S=4, dtype=BF, heads=list(range(8)) + list(range(56, 64)), do_std=0.1), id="c4"),
-    pytest.param(dict(B=8, Hq=32, Hkv=4, L=2048, D=128, W=512, S=16, dtype=FP, heads=list(range(8))), id="c5"),
+    pytest.param(dict(B=1, Hq=64, Hkv=8, L=8192, D=64, W=8192, S=0, dtype=BF), id="c3"),
+    pytest.param(dict(B=1, Hq=64, Hkv=8, L=32768, D=64, W=128, S=4, dtype=BF, do_std=0.1), id="c4"),
+    pytest.param(dict(B=8, Hq=32, Hkv=4, L=2048, D=128, W=512, S=16, dtype=FP), id="c5"),
 ])
 def test_baseline_configs(gpu, cfg):
     cfg = dict(cfg)

@@ -311,3 +311,91 @@ def test_transformers_gpt_oss_attention_padded_batch(gpu, fa, layer_idx):
     assert rel(ours.q_proj.weight.grad, ref.q_proj.weight.grad) < 2e-2
     assert rel(ours.k_proj.weight.grad, ref.k_proj.weight.grad) < 2e-2
     assert rel(ours.v_proj.weight.grad, ref.v_proj.weight.grad) < 2e-2
+
+
+def _gpt_oss_pair(fa, layer_idx, seed):
+    """An eager float32 GptOssAttention and the same weights in bf16 on the registered gfx950
+    attention function."""
+    mod = pytest.importorskip("transformers.models.gpt_oss.modeling_gpt_oss")
+    from transformers import GptOssConfig
+
+    name = fa.register_transformers("fa_gfx950")
+    cfg = dict(hidden_size=256, num_attention_heads=8, num_key_value_heads=2, head_dim=64, sliding_window=24,
+               num_hidden_layers=2, layer_types=["sliding_attention", "full_attention"], attention_bias=True,
+               vocab_size=128, intermediate_size=64, num_local_experts=4)
+    ref_cfg, our_cfg = GptOssConfig(**cfg), GptOssConfig(**cfg)
+    ref_cfg._attn_implementation = "eager"
+    our_cfg._attn_implementation = name
+    torch.manual_seed(seed)
+    ref = mod.GptOssAttention(ref_cfg, layer_idx).cuda()
+    with torch.no_grad():
+        for p in ref.parameters():
+            p.copy_((0.05 * torch.randn_like(p)).to(BF).float())
+        ref.sinks.copy_(torch.randn(8).to(BF).float())
+    ours = mod.GptOssAttention(our_cfg, layer_idx).cuda()
+    ours.load_state_dict(ref.state_dict())
+    return mod, ref, ours.to(BF), mod.GptOssRotaryEmbedding(ref_cfg).cuda()
+
+
+@pytest.mark.parametrize("layer_idx", [0, 1], ids=["sliding", "full"])
+def test_transformers_gpt_oss_packed_position_ids(gpu, fa, layer_idx):
+    """Padding-free finetuning: three sequences packed into one row, no mask, position ids that
+    restart at each sequence.  Equals the eager module run on each sequence alone -- no token
+    attends across a sequence boundary."""
+    mod, ref, ours, rope = _gpt_oss_pair(fa, layer_idx, seed=2)
+    lens = [40, 17, 35]
+    L = sum(lens)
+    pos = torch.cat([torch.arange(n) for n in lens]).unsqueeze(0).cuda()
+    x = torch.randn(1, L, 256, device="cuda").to(BF)
+    g = torch.randn(1, L, 256, device="cuda")
+    xo = x.clone().requires_grad_()
+    yo, _ = ours(xo, rope(xo, pos), None, position_ids=pos)
+    yo.backward(g.to(BF))
+    yr = torch.zeros(1, L, 256, device="cuda")
+    xr_grad = torch.zeros(1, L, 256, device="cuda")
+    lo = 0
+    for n in lens:
+        xb = x[:, lo:lo + n].float().requires_grad_()
+        pb = torch.arange(n, device="cuda").unsqueeze(0)
+        W = ref.sliding_window if ref.sliding_window is not None else n
+        add = torch.zeros(n, n, device="cuda").masked_fill(~naive.allowed_mask(n, W, 0, device="cuda"), float("-inf"))
+        yb, _ = ref(xb, rope(xb, pb), add.view(1, 1, n, n))
+        yb.backward(g[:, lo:lo + n])
+        yr[:, lo:lo + n] = yb.detach()
+        xr_grad[:, lo:lo + n] = xb.grad
+        lo += n
+    rel = lambda a, b: float((a.detach().float() - b.detach().float()).norm() / b.detach().float().norm())
+    assert rel(yo, yr) < 1e-2
+    assert rel(xo.grad, xr_grad) < 2e-2
+    assert rel(ours.sinks.grad, ref.sinks.grad) < 3e-2
+    assert rel(ours.q_proj.weight.grad, ref.q_proj.weight.grad) < 2e-2
+
+
+def test_padded_batch_later_layers_do_not_synchronise(gpu, fa):
+    """The host reads a padded batch's mask once (the first attention layer); the model's other
+    layers reuse what it found.  Later layers run with torch's sync debug mode set to "error"
+    (any device-to-host synchronisation raises) and give the same result as the first."""
+    mod, _, ours, rope = _gpt_oss_pair(fa, 0, seed=3)
+    B, L = 2, 80
+    mask = torch.zeros(B, L, dtype=torch.bool, device="cuda")
+    mask[0, :60] = True
+    mask[1, 13:] = True
+    pos = (mask.long().cumsum(-1) - 1).clamp(min=0)
+    x = torch.randn(B, L, 256, device="cuda").to(BF)
+    pe = rope(x, pos)
+    y1, _ = ours(x, pe, mask)  # first layer: reads the mask
+    torch.cuda.synchronize()
+    prev = torch.cuda.get_sync_debug_mode()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        outs = [ours(x, pe, mask)[0] for _ in range(3)]  # "later layers": same mask tensor
+    finally:
+        torch.cuda.set_sync_debug_mode(prev)
+    torch.cuda.synchronize()
+    for y in outs:
+        assert torch.equal(y, y1)
+    # and a new batch (another mask tensor) is read again
+    mask2 = mask.clone()
+    mask2[0, 60:70] = True
+    y3, _ = ours(x, pe, mask2)
+    assert not torch.equal(y3, y1)

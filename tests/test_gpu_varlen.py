@@ -168,3 +168,38 @@ def test_varlen_argument_errors(gpu):
         fa.flash_swda_with_sink_varlen(q, k, v, torch.tensor([0, 100], dtype=torch.int32).cuda(), None, 16, 1)
     with pytest.raises(ValueError, match="below the longest"):
         fa.flash_swda_with_sink_varlen(q, k, v, torch.tensor([0, 100]), 50, 16, 1)
+
+
+@pytest.mark.parametrize("cu,total", [
+    pytest.param([0, 300, 700], 900, id="trailing-rows"),
+    pytest.param([100, 400, 800], 900, id="leading-and-trailing-rows"),
+    pytest.param([0, 500], 500, id="all-rows-covered"),
+])
+def test_varlen_rows_outside_every_sequence(gpu, cu, total):
+    """Packed rows that belong to no sequence ([0, cu[0]) and [cu[B], total)) come back as o = 0,
+    lse = -inf and zero gradients -- not whatever the allocator held (the memory is filled with
+    NaN first).  Rows inside the sequences equal a call on exactly those rows, bit for bit."""
+    ops = load_mod("_ops")
+    Hq, Hkv, D, W, S = 8, 2, 64, 64, 4
+    print(f"case cu={cu} total={total}", flush=True)
+    q, k, v, do = packed_inputs(total, Hq, Hkv, D, BF, seed=21)
+    junk = torch.full((1 << 24,), float("nan"), device=q.device)  # dirty the caching allocator's blocks
+    del junk
+    cu_dev = torch.tensor(cu, dtype=torch.int32, device=q.device)  # device offsets: used as given
+    max_len = max(b - a for a, b in zip(cu[:-1], cu[1:]))
+    o, lse = ops.forward_varlen(q, k, v, cu_dev, max_len, W, S, 0.125)
+    dq, dk, dv = ops.backward_varlen(q, k, v, o, lse, do, cu_dev, max_len, W, S, 0.125)
+    torch.cuda.synchronize()
+    lo, hi = cu[0], cu[-1]
+    outside = torch.ones(total, dtype=torch.bool)
+    outside[lo:hi] = False
+    for name, t in (("o", o), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert bool((t[outside.cuda()] == 0).all()), name
+    assert bool((lse[:, outside.cuda()] == float("-inf")).all())
+    # the covered rows: the same call on the rows [lo, hi) alone, offsets shifted to start at 0
+    cu2 = torch.tensor([c - lo for c in cu], dtype=torch.int32, device=q.device)
+    sl = lambda t: t[lo:hi].contiguous()
+    o2, lse2 = ops.forward_varlen(sl(q), sl(k), sl(v), cu2, max_len, W, S, 0.125)
+    dq2, dk2, dv2 = ops.backward_varlen(sl(q), sl(k), sl(v), o2, lse2, sl(do), cu2, max_len, W, S, 0.125)
+    assert torch.equal(o[lo:hi], o2) and torch.equal(lse[:, lo:hi], lse2)
+    assert torch.equal(dq[lo:hi], dq2) and torch.equal(dk[lo:hi], dk2) and torch.equal(dv[lo:hi], dv2)
