@@ -30,6 +30,8 @@ FA_ERR_WORKSPACE = -7
 FA_ERR_LAUNCH = -8
 FA_ERR_OVERFLOW = -9
 FA_ERR_SCALE = -10
+FA_ERR_SCRATCH = -11
+FA_SCRATCH_BYTES = 128 << 20
 
 # Every function the header declares; the tests check that the library exports each one.
 EXPORTS = (
@@ -37,6 +39,7 @@ EXPORTS = (
     "fa_bwd",
     "fa_bwd_dq",
     "fa_bwd_dkdv",
+    "fa_bwd_scratch",
     "fa_fwd_sinks",
     "fa_bwd_sinks",
     "fa_fwd_varlen",
@@ -131,6 +134,8 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(L, name)
                 fn.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
                 fn.restype = ctypes.c_int
+            L.fa_bwd_scratch.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_void_p]
+            L.fa_bwd_scratch.restype = ctypes.c_int
             L.fa_fwd_sinks.argtypes = [ctypes.POINTER(FwdParams), ctypes.c_void_p, ctypes.c_void_p]
             L.fa_fwd_sinks.restype = ctypes.c_int
             L.fa_bwd_sinks.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,

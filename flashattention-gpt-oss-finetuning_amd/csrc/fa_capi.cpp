@@ -512,6 +512,7 @@ const char* fa_strerror(int status) {
     case FA_ERR_LAUNCH: return "HIP kernel launch failed";
     case FA_ERR_OVERFLOW: return "problem size exceeds the kernels' index range";
     case FA_ERR_SCALE: return "softmax_scale (and the fp8 dequantisation factors) must be finite";
+    case FA_ERR_SCRATCH: return "the problem needs more backward workspace than the library's scratch buffer (FA_SCRATCH_BYTES) holds; use fa_bwd with a workspace";
   }
   return "unknown fa_status";
 }

@@ -19,13 +19,14 @@
  *
  * Rules shared by every entry point:
  *   - the library never allocates or frees device memory; the caller passes every buffer,
- *     including the backward workspace sized by fa_bwd_workspace_bytes();
+ *     including the backward workspace sized by fa_bwd_workspace_bytes() (fa_bwd_scratch uses
+ *     the library's own static per-GPU buffer instead);
  *   - launches are asynchronous on `stream` (a hipStream_t; NULL means the legacy default
  *     stream); nothing synchronises the host;
  *   - arguments are validated on the host before any HIP call; on failure a negative FA_ERR_*
  *     code is returned and nothing is launched.  fa_strerror() names each code;
- *   - the library holds no mutable global state, so concurrent calls on different streams are
- *     safe.
+ *   - apart from fa_bwd_scratch's buffer, the library holds no mutable global state, so
+ *     concurrent calls on different streams are safe.
  */
 #ifndef FA_GFX950_H
 #define FA_GFX950_H
@@ -56,8 +57,12 @@ enum fa_status {
   FA_ERR_WORKSPACE = -7,   /* workspace NULL or smaller than fa_bwd_workspace_bytes() */
   FA_ERR_LAUNCH = -8,      /* a HIP launch failed */
   FA_ERR_OVERFLOW = -9,    /* a size or element offset does not fit the kernels' index math */
-  FA_ERR_SCALE = -10       /* softmax_scale is NaN or infinite */
+  FA_ERR_SCALE = -10,      /* softmax_scale is NaN or infinite */
+  FA_ERR_SCRATCH = -11     /* fa_bwd_scratch: the problem needs more workspace than FA_SCRATCH_BYTES */
 };
+
+/* Size of the library's own device scratch buffer used by fa_bwd_scratch (per GPU). */
+#define FA_SCRATCH_BYTES (128u << 20) /* 128 MiB */
 
 /* Forward pass.  Replaces the launch in FlashSWDAWithSink.forward
  * (flash_attention_gpt_oss.py:341-385) and the Triton _forward_kernel of the benchmark
@@ -135,6 +140,18 @@ int fa_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void
  * must run after fa_bwd_dq on the same workspace, in stream order. */
 int fa_bwd_dq(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
 int fa_bwd_dkdv(const fa_bwd_params* p, void* workspace, size_t workspace_bytes, void* stream);
+
+/* fa_bwd without a workspace argument, for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving or training loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference (its backward allocates fp32 staging tensors,
+ * flash_attention_gpt_oss.py:397-400).  The workspace is the library's own static device buffer
+ * of FA_SCRATCH_BYTES bytes, one per GPU, held from the library's first use on that GPU until the
+ * process ends; the call itself allocates and frees nothing.  Same arguments, checks, kernels and
+ * results as fa_bwd (bitwise).  Returns FA_ERR_SCRATCH when fa_bwd_workspace_bytes() of the
+ * problem exceeds FA_SCRATCH_BYTES.  Every call on one GPU shares that GPU's buffer: calls that
+ * overlap in time on one GPU (concurrent streams, or host threads launching without ordering)
+ * race on it and must be serialised by the caller; calls in one stream are ordered and safe. */
+int fa_bwd_scratch(const fa_bwd_params* p, void* stream);
 
 /* Learned attention sinks (GPT-OSS).  The reference has no such entry point: its sinks are the
  * first S key positions (benchmark_backward_speed.py:45, README.md:15).  GPT-OSS models instead

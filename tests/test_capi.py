@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_strerror():
     L = _lib.lib()
     assert L.fa_version() == 10400
-    codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10]
+    codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11]
     texts = [_lib.strerror(c) for c in codes]
     assert len(set(texts)) == len(codes)
     assert _lib.strerror(12345) == "unknown fa_status"
@@ -301,3 +301,20 @@ def test_fp8_entry_point_rejects_before_any_hip_call(entry):
     assert call(_fwd_params(dtype=F8), sinks=ctypes.c_void_p(258)) == _lib.FA_ERR_ALIGN
     # the 16-bit entry points do not take the e4m3 code
     assert L.fa_check_fwd(ctypes.byref(_fwd_params(dtype=F8))) == _lib.FA_ERR_DTYPE
+
+
+def test_scratch_entry_point_rejects_before_any_hip_call():
+    """fa_bwd_scratch checks its arguments like fa_bwd, then refuses a problem whose workspace
+    exceeds the library's static buffer (FA_ERR_SCRATCH), all before any HIP call."""
+    L = _lib.lib()
+    assert L.fa_bwd_scratch(None, None) == _lib.FA_ERR_NULL
+    assert L.fa_bwd_scratch(ctypes.byref(_bwd_params(head_dim=48)), None) == _lib.FA_ERR_HEAD_DIM
+    assert L.fa_bwd_scratch(ctypes.byref(_bwd_params(window=0, sink=0)), None) == _lib.FA_ERR_MASK
+    # 64 heads x 2^20 rows of delta alone is 256 MiB > FA_SCRATCH_BYTES
+    big = 1 << 20
+    st = (64 * big * 64, big * 64, 64)
+    p = _bwd_params(heads_q=64, heads_kv=8, seqlen=big, q_stride=st, o_stride=st, do_stride=st, dq_stride=st,
+                    lse_stride=(64 * big, big, 1))
+    assert L.fa_check_bwd(ctypes.byref(p)) == _lib.FA_OK
+    assert L.fa_bwd_workspace_bytes(1, 64, 8, big, 64, 16, 4) > _lib.FA_SCRATCH_BYTES
+    assert L.fa_bwd_scratch(ctypes.byref(p), None) == _lib.FA_ERR_SCRATCH
