@@ -18,6 +18,7 @@ HEADER_PATH = os.path.join(os.path.dirname(PKG_DIR), "include", "fa_gfx950.h")
 FA_DTYPE_BF16 = 1
 FA_DTYPE_F16 = 2
 FA_DTYPE_FP8_E4M3 = 3
+FA_DTYPE_F32 = 4
 
 FA_OK = 0
 FA_ERR_NULL = -1

@@ -19,7 +19,7 @@ import torch
 
 from . import _lib
 
-_DTYPES = {torch.bfloat16: _lib.FA_DTYPE_BF16, torch.float16: _lib.FA_DTYPE_F16}
+_DTYPES = {torch.bfloat16: _lib.FA_DTYPE_BF16, torch.float16: _lib.FA_DTYPE_F16, torch.float32: _lib.FA_DTYPE_F32}
 _I32_MIN, _I32_MAX = -(2 ** 31), 2 ** 31 - 1
 
 
@@ -28,8 +28,11 @@ def _i32(x: int) -> int:
 
 
 def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+    """t itself when the kernels can read it in place (head-dim stride 1, the other strides whole
+    multiples of 16 bytes, 16-byte aligned base), else a contiguous copy."""
     st = t.stride()
-    if st[3] != 1 or (t.data_ptr() & 15) or (st[0] & 7) or (st[1] & 7) or (st[2] & 7):
+    m = 16 // t.element_size() - 1
+    if st[3] != 1 or (t.data_ptr() & 15) or (st[0] & m) or (st[1] & m) or (st[2] & m):
         t = t.contiguous()
         if t.data_ptr() & 15:
             t = t.clone(memory_format=torch.contiguous_format)
@@ -45,7 +48,7 @@ def _check(tensors, names):
         )
     dt = tensors[0].dtype
     if dt not in _DTYPES:
-        raise ValueError(f"{names[0]} has dtype {dt}; supported dtypes are bfloat16 and float16")
+        raise ValueError(f"{names[0]} has dtype {dt}; supported dtypes are bfloat16, float16 and float32")
     for t, n in zip(tensors, names):
         if t.dim() != 4:
             raise ValueError(f"{n} must be 4-D [B, H, L, D], got shape {tuple(t.shape)}")

@@ -23,7 +23,8 @@ struct Args {
   void* dk;
   void* dv;
   // backward workspace
-  float* delta;      // [B][Hq][Lp] fp32, Lp = L rounded up to 32
+  float* delta;      // row statistics: [B][Hq][Lp / 32][lse * log2(e) x 32, -delta x 32] fp32, Lp = L
+                     // rounded up to 32 (written by the dQ kernel, read by the dK/dV kernel)
   float* partial;    // sink-key partial sums, see fa_bwd.hip
   // learned per-head sink logits (GPT-OSS): NULL, or [Hq] fp32 logits that join every row's
   // softmax denominator without a value row
@@ -123,5 +124,10 @@ hipError_t launch_bwd_dq(const Args& a, int dtype, int D, int hpw, hipStream_t s
 hipError_t launch_bwd_dkdv(const Args& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_bwd_sink_logits(const Args& a, hipStream_t stream);  // after launch_bwd_dq
 hipError_t launch_varlen_tail(const TailArgs& t, hipStream_t stream);
+// float32 inputs (fa_f32.hip).  The dK/dV launch reads n_kblocks (32-key tiles), nsp (sink tiles
+// that may be split), n_chunks and chunk_rows (their chunk workgroups) and launches the fold.
+hipError_t launch_fwd_f32(const Args& a, int D, hipStream_t stream);
+hipError_t launch_bwd_dq_f32(const Args& a, int D, hipStream_t stream);
+hipError_t launch_bwd_dkdv_f32(const Args& a, int D, hipStream_t stream);
 
 }  // namespace fa

@@ -203,7 +203,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
     const float lse2 = q < L ? lse_next * kLog2e : __builtin_inff();
     {
       KArgs& A = args_fresh();
-      if (q < L && hf == 0) A.delta[(int64_t(t.b) * A.Hq + t.hw) * A.Lp + q] = delta;
+      // the row statistics of the dK/dV kernel: per 32-row block, lse * log2(e) for the 32 rows,
+      // then -delta (rows past L: +inf and 0, so that their P and dS there are exactly 0)
+      if (hf == 0 && wave_active) {  // (an active wave's rows are all < Lp)
+        float* st = A.delta + ((int64_t(t.b) * A.Hq + t.hw) * (A.Lp / 32) + qw / 32) * 64;
+        st[r32] = lse2;
+        st[32 + r32] = ndelta;
+      }
       if (A.sink_logits && wave_active) {
         // learned sink: d sink = -sum over rows of P_sink * delta, P_sink = 2^(sink*log2e - lse2);
         // one partial per 32-row block, summed in a fixed order by bwd_sink_logit_kernel
@@ -443,9 +449,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
 // ---------------------------------------------------------------------------------------------
 // dK / dV (key-major).  A workgroup owns 64 keys of one KV head; wave (kh, hh) = (wave & 1,
 // wave >> 1) owns the 32-key half kh and takes head slot hh of every step.  A step stages two
-// (query head, 32-row block) items -- Q and dO rows plus their lse/delta -- in LDS, shared by the
-// two waves of each slot; the next step's items are fetched into registers while this step
-// computes.  Per item and wave: S = Q K^T and dP = dO V^T in C layout (lane = key column, 16
+// (query head, 32-row block) items -- Q and dO rows plus their lse * log2(e) and -delta -- in LDS,
+// shared by the two waves of each slot; they arrive by DMA, issued a few steps ahead into a ring
+// of LDS stages.  Per item and wave: S = Q K^T and dP = dO V^T in C layout (lane = key column, 16
 // query rows per lane), P and dS elementwise, then dV^T += dO^T P and dK^T += Q^T dS with P/dS
 // straight from registers and dO^T/Q^T read transposed from the row-major tiles
 // (ds_read_b64_tr_b16).  The two head slots' partial sums are added in LDS at the end.
@@ -464,9 +470,9 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   constexpr int KS = D / 16;
   constexpr int DB = D >= 32 ? D / 32 : 1;
   constexpr int TILE = 32 * D;               // 32 rows of Q or dO, swizzled row-major
-  constexpr int SLOT = 2 * TILE + 128;       // Q, dO, then lse2[32] and delta[32] as fp32
+  constexpr int SLOT = 2 * TILE + 128;       // Q, dO, then lse2[32] and -delta[32] as fp32
   constexpr int STAGE = 2 * SLOT;            // two items per step
-  constexpr int NSTG = 3;                    // LDS stages: compute, landed, in flight
+  constexpr int NSTG = D == 128 ? 3 : 4;     // LDS stages: see the staging below
   constexpr int CPR = D / 8;                 // 16-byte chunks per row
   constexpr int RED = 2 * 2 * DB * 16 * 64;  // fp32 partials of the two hh = 1 waves
   constexpr int LDS_ELEMS = (NSTG * STAGE > 2 * RED) ? NSTG * STAGE : 2 * RED;
@@ -541,17 +547,21 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   const int n_qp = (n_qb + 1) / 2;
   const int n_steps = G * n_qp;
 
-  // ---- staging.  The four 32-row tiles of a step (slot 0 Q, slot 0 dO, slot 1 Q, slot 1 dO)
-  // go straight from HBM into an LDS stage by DMA (buffer_load ... lds): wave w loads tile w,
-  // IPT instructions of 64 lanes x 16 bytes, each writing 1 KiB of the swizzled tile in lane
-  // order -- so lane l of instruction p loads the global chunk that the swizzle places at
-  // 16-byte position 64p + l.  Loads go through buffer resources spanning one query head's rows
-  // [0, L) (rows past L read as zero; a head slice is < 2^31 bytes, checked by the C ABI);
-  // descriptors change only with the head.  The row statistics (lse, delta: one value per
-  // thread of the first two waves) take the register path, transformed on their way to LDS.
-  // Three stages rotate: the step being computed, the next one (landed), and the one after
-  // (in flight), so a step's tiles have two steps of compute to arrive. ------------------------
+  // ---- staging.  Everything a step reads goes straight from memory into an LDS stage by DMA
+  // (buffer_load ... lds): the four 32-row tiles (slot 0 Q, slot 0 dO, slot 1 Q, slot 1 dO; wave w
+  // loads tile w, IPT instructions of 64 lanes x 16 bytes, each writing 1 KiB of the swizzled tile
+  // in lane order -- lane l of instruction p loads the global chunk that the swizzle places at
+  // 16-byte position 64p + l) and each slot's row statistics (one 64-lane dword instruction: the
+  // dQ kernel stores a 32-row block's lse * log2(e) and -delta as 64 consecutive floats, exactly
+  // the slot's statistics area; waves w and w + 2 both load slot w % 2's, the same bytes to the same
+  // place, so that every wave issues IPT + 1 loads per step).  Loads go through buffer resources
+  // spanning one query head's rows [0, L) (rows past L read as zero; a head slice is < 2^31 bytes,
+  // checked by the C ABI); descriptors change only with the head.
+  // NSTG stages rotate and loads are issued NSTG - 1 steps ahead, so the loads of a step have
+  // NSTG - 2 steps of compute to land.
   constexpr int IPT = 32 * D * 2 / 1024;         // DMA instructions per tile (1 KiB each)
+  constexpr int PER = IPT + 1;                   // loads per wave and step
+  static_assert(PER <= 63, "vmcnt immediate");
   const int t_slot = wave >> 1, t_kind = wave & 1;  // this wave's tile: slot, Q (0) or dO (1)
   const int64_t t_rs = t_kind ? a.sdo[2] : a.sq[2];  // row stride of the tile's tensor
   uint32_t dma_off[IPT];
@@ -564,73 +574,37 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   }
   const char* qslice = reinterpret_cast<const char*>(a.q) + 2 * slice_off(a.sq, b, kvh * G, sq.row);
   const char* dslice = reinterpret_cast<const char*>(a.dout) + 2 * slice_off(a.sdo, b, kvh * G, sq.row);
-  const char* lslice = reinterpret_cast<const char*>(a.lse + slice_off(a.slse, b, kvh * G, sq.row));
-  const char* tslice = reinterpret_cast<const char*>(a.delta + (int64_t(b) * a.Hq + int64_t(kvh) * G) * a.Lp);
+  // row statistics of (b, head kvh G + fh): Lp / 32 blocks of 64 floats
+  const int nblk = a.Lp / 32;
+  const char* sslice = reinterpret_cast<const char*>(a.delta + (int64_t(b) * a.Hq + int64_t(kvh) * G) * nblk * 64);
   const char* tile_slice = t_kind ? dslice : qslice;
   const int64_t t_hs = t_kind ? a.sdo[1] : a.sq[1];  // head stride of the tile's tensor
   const uint32_t nt_bytes = span_bytes(L, t_rs, D);
-  const uint32_t nl = span_f32(L, a.slse[2]), nt = uint32_t(L * 4);
-  // bytes per 32-row block
-  const uint32_t bt = uint32_t(64 * t_rs), bl = uint32_t(128 * a.slse[2]);
-  // stats: thread tid < 128 loads row tid % 32 of (slot tid / 64, kind (tid / 32) % 2).  Every
-  // thread issues both loads (threads >= 128 at an offset past any buffer, which reads 0), so
-  // the number of loads in flight is the same on every path.
-  const int st_slot = (tid >> 6) & 1, st_kind = (tid >> 5) & 1, st_row = tid & 31;
-  const uint32_t st_far = tid < 128 ? 0u : 0x80000000u;
-  const uint32_t lse_off = uint32_t(int64_t(st_row) * 4 * a.slse[2]) | st_far, dlt_off = uint32_t(st_row * 4) | st_far;
-  // Register part of a step: the two row statistics and the step's first row.
-  struct Stage {
-    float stat, stat2;  // lse, delta
-    int q0;             // first row of slot 0
-  };
-  Stage sa, sb;
+  const uint32_t bt = uint32_t(64 * t_rs);  // tile bytes per 32-row block
+  const int s_slot = wave & 1;              // the slot whose statistics this wave loads
   // fetch side: the step (fh, fp) being loaded and the descriptors of head fh
   int fh = 0, fp = 0;
-  rsrc_t rtile, rl, rt;
+  rsrc_t rtile, rstat;
   auto set_head = [&]() {
     rtile = make_rsrc(tile_slice + int64_t(fh) * 2 * t_hs, nt_bytes);
-    rl = make_rsrc(lslice + int64_t(fh) * 4 * a.slse[1], nl);
-    rt = make_rsrc(tslice + int64_t(fh) * 4 * a.Lp, nt);
+    rstat = make_rsrc(sslice + int64_t(fh) * nblk * 256, uint32_t(nblk * 256));
   };
-  // issues the loads of step (fh, fp) -- tiles into LDS stage `buf`, statistics into st -- and
-  // moves the fetch side to the next step
-  auto gload = [&](Stage& st, int buf) {
+  // issues the loads of step (fh, fp) into LDS stage `buf` and moves the fetch side to the next
+  // step (loads past the last step read the last head's rows or zeros into a stage that is never
+  // computed, so every step keeps the same number of loads in flight)
+  auto issue = [&](int buf) {
     const uint32_t qb0 = uint32_t(qb_lo + 2 * fp);  // block of slot 0
     const uint32_t blk_off = (qb0 + uint32_t(t_slot)) * bt;
     uint16_t* dst = lds + buf * STAGE + t_slot * SLOT + t_kind * TILE;
 #pragma unroll
     for (int p = 0; p < IPT; ++p)
       buf_dma16(rtile, dst + 512 * p, dma_off[p] + blk_off);
-    // raw values: any arithmetic on them here would make the wave wait for the loads now
-    const uint32_t blk = qb0 + uint32_t(st_slot);
-    st.stat = buf_ldf(rl, lse_off + blk * bl);
-    st.stat2 = buf_ldf(rt, dlt_off + blk * 128u);
-    st.q0 = 32 * int(qb0);
+    buf_dma4(rstat, lds + buf * STAGE + s_slot * SLOT + 2 * TILE, (qb0 + uint32_t(s_slot)) * 256u + 4u * lane);
     if (++fp == n_qp) {
       fp = 0;
       ++fh;
       if (fh < G) set_head();
     }
-  };
-  // lse -> lse * log2(e) (+inf for rows past L, which read 0: their P is exactly 0);
-  // delta -> -delta, the initial value of the dP accumulator
-  auto sstore = [&](const Stage& st, int buf) {
-    if (tid < 128) {
-      const int qrow = st.q0 + 32 * st_slot + st_row;
-      const float v = st_kind ? -st.stat2 : (qrow < L ? st.stat * kLog2e : __builtin_inff());
-      reinterpret_cast<float*>(lds + buf * STAGE + st_slot * SLOT + 2 * TILE)[st_kind * 32 + st_row] = v;
-    }
-  };
-  // End of a step: this wave's loads of the next step have landed (the step after may still be
-  // in flight: its IPT DMA instructions and 2 statistics loads), its statistics are stored, and
-  // every wave has passed this point.  Waits and barrier are explicit: the compiler would
-  // otherwise also wait for the step still in flight.
-  auto step_end = [&]() {
-    static_assert(IPT + 2 <= 15, "vmcnt immediate");
-    if constexpr (IPT + 2 == 3) asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr (IPT + 2 == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr (IPT + 2 == 6) asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   };
 
   // Per-lane constants of the compute.  The mask is one unsigned compare per element:
@@ -642,16 +616,19 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   else lim = key < S ? (partial_block ? unsigned(max(wqhi - key, 0)) : 0x80000000u) : unsigned(W);
   const int mref = is_chunk ? qlo : key;  // mask coordinate: row - mref
 
-  // One item of this wave: the (head, block) pair cp of the step in LDS stage `buf`, slot hh.
-  auto compute = [&](int buf, int cp) {
+  // Does this wave compute the item of block pair cp in slot hh?
+  auto needed = [&](int cp) {
     const int qbi = 2 * cp + hh;
     const int qr0 = 32 * (qb_lo + qbi);
-    if (!(wave_on && qbi < n_qb && qr0 + 32 > wqlo && qr0 < wqhi && kv_half_needs(qr0, ks0, L, W, S))) return;
+    return wave_on && qbi < n_qb && qr0 + 32 > wqlo && qr0 < wqhi && kv_half_needs(qr0, ks0, L, W, S);
+  };
+  // The score products of an item from LDS stage `buf`: S = Q K^T and dP - delta = dO V^T - delta
+  // (the accumulator starts from -delta), lane = key column, 16 query rows per lane.
+  auto scores = [&](int buf, f32x16& sacc, f32x16& dpacc) {
     const uint16_t* Qt = lds + buf * STAGE + hh * SLOT;
     const uint16_t* Dt = Qt + TILE;
-    const float* lse2 = reinterpret_cast<const float*>(Qt + 2 * TILE);
-    const float* ndlt = lse2 + 32;  // -delta
-    f32x16 sacc = f32x16{}, dpacc;
+    const float* ndlt = reinterpret_cast<const float*>(Qt + 2 * TILE) + 32;  // -delta
+    sacc = f32x16{};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const f32x4 d4 = *reinterpret_cast<const f32x4*>(ndlt + 8 * j + 4 * hf);
@@ -662,12 +639,20 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
     for (int ks = 0; ks < KS; ++ks) {
       const int a_off = swz_off<D>(r32, hf * (D / 2) + 8 * ks);
       sacc = E::mfma(lds16(Qt + a_off), kf[ks], sacc);
-      dpacc = E::mfma(lds16(Dt + a_off), vf[ks], dpacc);  // dP - delta
+      dpacc = E::mfma(lds16(Dt + a_off), vf[ks], dpacc);
     }
+  };
+  // The rest of an item, from its score products and LDS stage `buf`: P = exp2(s c - lse2) and
+  // dS = P (dP - delta) elementwise (masked or not), then dV^T += dO^T P and dK^T += Q^T dS with P
+  // and dS straight from registers and dO^T / Q^T read transposed from the row-major tiles.
+  auto finish = [&](int buf, int cp, const f32x16& sacc, const f32x16& dpacc) {
+    const int qr0 = 32 * (qb_lo + 2 * cp + hh);
+    const uint16_t* Qt = lds + buf * STAGE + hh * SLOT;
+    const uint16_t* Dt = Qt + TILE;
+    const float* lse2 = reinterpret_cast<const float*>(Qt + 2 * TILE);
     const bool full = !is_chunk && qr0 >= wqlo && qr0 + 32 <= wqhi && tile_full(ks0, qr0, W, S);
     const int m0 = qr0 + 4 * hf - mref;  // mask coordinate of register e = 0
     float p[16], ds[16];
-    // P = exp2(s*c - lse2) and dS = P (dP - delta); MASK selects the masked variant
     auto elementwise = [&](auto mask_tag) {
       constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
@@ -702,37 +687,26 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   // Descriptors are built before any load, whatever the number of steps (a workgroup can own
   // no items: a chunk whose rows all lie inside the window).
   set_head();
-  int cb = 0;  // LDS stage of the step being computed; (cb + 1) % 3 holds the next step
+  // Stage s % NSTG holds step s; the loads of step s + NSTG - 1 go into stage (s - 1) % NSTG, whose
+  // last reader (step s - 1) is behind the barrier at the start of step s; the wait before that
+  // barrier is for this wave's own loads of step s (the explicit wait: the compiler does not track
+  // the DMA writes into LDS and would otherwise wait for every load in flight).
   if (n_steps > 0) {
-    gload(sa, 0);  // step 0
-    gload(sb, 1);  // step 1
-    // step 0 landed (step 1 may be in flight)
-    if constexpr (IPT + 2 == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
-    else if constexpr (IPT + 2 == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else if constexpr (IPT + 2 == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
-    sstore(sa, 0);
-    step_end();
-  }
-  // Step s computes stage cb, issues the loads of step s + 2 into stage (cb + 2) % 3 (last read
-  // at step s - 1, before the barrier that ended it) and stores the statistics of step s + 1.
-  // Loads past the last step are issued anyway (they read the last head's rows or zeros into a
-  // stage that is never computed), so every step keeps the same number of loads in flight.
-  int cp = 0;  // block pair of the step being computed
-  for (int step = 0; step < n_steps; step += 2) {
-    gload(sa, cb == 0 ? 2 : cb - 1);
-    compute(cb, cp);
-    if (++cp == n_qp) cp = 0;
-    cb = cb == 2 ? 0 : cb + 1;
-    sstore(sb, cb);
-    step_end();
-    if (step + 1 >= n_steps) break;
-    gload(sb, cb == 0 ? 2 : cb - 1);
-    compute(cb, cp);
-    if (++cp == n_qp) cp = 0;
-    cb = cb == 2 ? 0 : cb + 1;
-    sstore(sa, cb);
-    step_end();
+    // loads NSTG - 1 steps ahead; step s waits for its own
+    for (int k = 0; k < NSTG - 1; ++k) issue(k);
+    int cp = 0, cur = 0, nxt = NSTG - 1;  // stage of step s, stage of step s + NSTG - 1
+    for (int s = 0; s < n_steps; ++s) {
+      wait_vm_lgkm0_barrier<(NSTG - 2) * PER>();  // step s landed everywhere
+      issue(nxt);
+      if (needed(cp)) {
+        f32x16 sacc, dpacc;
+        scores(cur, sacc, dpacc);
+        finish(cur, cp, sacc, dpacc);
+      }
+      cp = cp + 1 == n_qp ? 0 : cp + 1;
+      cur = cur + 1 == NSTG ? 0 : cur + 1;
+      nxt = nxt + 1 == NSTG ? 0 : nxt + 1;
+    }
   }
 
   // ---- add the two head slots' partial sums (hh = 0 gets hh = 1's), fixed order ---------------

@@ -38,12 +38,15 @@ bool slice_fits(const int64_t s[3], int L, int D, int elem_bytes) {
   return (int64_t(L - 1) * s[2] + D) * elem_bytes < (int64_t(1) << 31);
 }
 
+// bytes per element of q/k/v/o/dout/dq/dk/dv for a 16-bit or float32 call
+int elem_bytes(int32_t dtype) { return dtype == FA_DTYPE_F32 ? 4 : 2; }
+
 int check_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t L, int32_t D, int32_t W, int32_t S,
                  float scale, int32_t dtype) {
   if (B < 1 || Hq < 1 || Hkv < 1 || L < 1) return FA_ERR_SHAPE;
   if (Hq % Hkv != 0) return FA_ERR_SHAPE;
   if (D != 16 && D != 32 && D != 64 && D != 128) return FA_ERR_HEAD_DIM;
-  if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F16) return FA_ERR_DTYPE;
+  if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_F32) return FA_ERR_DTYPE;
   if (W < 1 && S < 1) return FA_ERR_MASK;
   if (!std::isfinite(scale)) return FA_ERR_SCALE;
   if (int64_t(L) > kMaxSeq) return FA_ERR_OVERFLOW;
@@ -102,9 +105,10 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // per-32-row-block partial sums of the learned sink logits' gradient: [B][Hq][Lp / 32] fp32
 size_t dsink_part_bytes(int B, int Hq, int L) { return align256(size_t(B) * Hq * ((size_t(L) + 31) / 32) * sizeof(float)); }
 
+// row statistics of the backward: [B][Hq][Lp / 32][lse * log2(e) x 32, -delta x 32] fp32
 size_t delta_bytes(int B, int Hq, int L) {
   const size_t Lp = (size_t(L) + 31) / 32 * 32;
-  return align256(size_t(B) * Hq * Lp * sizeof(float));
+  return align256(size_t(B) * Hq * Lp * 2 * sizeof(float));
 }
 
 // fp32 partial sums of the sink rows: [B * Hkv][nsp][n_chunks + 1 slots][dK, dV][srows][D]
@@ -116,6 +120,36 @@ size_t partial_bytes(int B, int Hkv, int D, const SinkPlan& sp) {
 // per tile; a run of tiles writes the slot of its first tile)
 size_t dq_sink_slot_bytes(int B, int Hq, int Hkv, int L, int D, const SinkPlan& sp) {
   return sp.dq ? align256(size_t(dq_tiles(B, Hq, Hkv, L)) * 2 * sp.srows * D * sizeof(float)) : 0;
+}
+
+// float32 backward: 32-key tiles; the tiles holding sink keys whose rows extend past their window
+// (kv32_row_end in fa_f32.hip: min(L, 32 kt + 31 + max(W, 1))) split those rows into chunk
+// workgroups of kF32ChunkRows rows, with fp32 partials [B * Hkv][nsp][n_chunks + 1][dK, dV][32][D].
+constexpr int kF32ChunkRows = 256;
+struct F32Plan {
+  int n_kt, nsp, n_chunks;
+};
+F32Plan f32_plan(int L, int W, int S) {
+  W = W < 0 ? 0 : (W > L ? L : W);
+  S = S < 0 ? 0 : (S > L ? L : S);
+  F32Plan p;
+  p.n_kt = (L + 31) / 32;
+  const int row_end0 = fa::imin(L, 31 + fa::imax(W, 1));  // tile 0's window rows end first
+  p.n_chunks = (S > 0 && row_end0 < L) ? (L - row_end0 + kF32ChunkRows - 1) / kF32ChunkRows : 0;
+  p.nsp = p.n_chunks > 0 ? (S + 31) / 32 : 0;
+  return p;
+}
+size_t f32_partial_bytes(int B, int Hkv, int D, const F32Plan& fp) {
+  return align256(size_t(B) * Hkv * fp.nsp * (fp.n_chunks + 1) * 2 * 32 * D * sizeof(float));
+}
+// The workspace after the row statistics and the learned-sink partials: the sink-key partials
+// and dQ-kernel slots of the 16-bit backward, or the float32 backward's partials (whichever is
+// larger, so one size serves every dtype).
+size_t partial_region_bytes(int B, int Hq, int Hkv, int L, int D, int W, int S) {
+  const SinkPlan sp = sink_plan(L, W, S);
+  const size_t b16 = partial_bytes(B, Hkv, D, sp) + dq_sink_slot_bytes(B, Hq, Hkv, L, D, sp);
+  const size_t b32 = f32_partial_bytes(B, Hkv, D, f32_plan(L, W, S));
+  return b16 > b32 ? b16 : b32;
 }
 
 void copy3(int64_t dst[3], const int64_t src[3]) {
@@ -157,13 +191,14 @@ int fa_check_fwd(const fa_fwd_params* p) {
   if (rc != FA_OK) return rc;
   if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o) || !aligned4(p->lse))
     return FA_ERR_ALIGN;
-  if (!strides_ok(p->q_stride) || !strides_ok(p->k_stride) || !strides_ok(p->v_stride) ||
-      !strides_ok(p->o_stride) || !lse_strides_ok(p->lse_stride))
+  const int eb = elem_bytes(p->dtype);
+  if (!strides_ok(p->q_stride, eb) || !strides_ok(p->k_stride, eb) || !strides_ok(p->v_stride, eb) ||
+      !strides_ok(p->o_stride, eb) || !lse_strides_ok(p->lse_stride))
     return FA_ERR_ALIGN;
   // q, k and v are staged through buffer resources with 32-bit byte offsets inside one
   // (batch, head) slice; o and lse are written through 64-bit addresses
   const int L = p->seqlen, D = p->head_dim;
-  if (!slice_fits(p->q_stride, L, D, 2) || !slice_fits(p->k_stride, L, D, 2) || !slice_fits(p->v_stride, L, D, 2))
+  if (!slice_fits(p->q_stride, L, D, eb) || !slice_fits(p->k_stride, L, D, eb) || !slice_fits(p->v_stride, L, D, eb))
     return FA_ERR_OVERFLOW;
   return FA_OK;
 }
@@ -179,15 +214,16 @@ int fa_check_bwd(const fa_bwd_params* p) {
   for (const void* x : ptrs)
     if (!aligned16(x)) return FA_ERR_ALIGN;
   if (!aligned4(p->lse)) return FA_ERR_ALIGN;
-  if (!strides_ok(p->q_stride) || !strides_ok(p->k_stride) || !strides_ok(p->v_stride) ||
-      !strides_ok(p->o_stride) || !strides_ok(p->do_stride) || !lse_strides_ok(p->lse_stride) ||
-      !strides_ok(p->dq_stride) || !strides_ok(p->dk_stride) || !strides_ok(p->dv_stride))
+  const int eb = elem_bytes(p->dtype);
+  if (!strides_ok(p->q_stride, eb) || !strides_ok(p->k_stride, eb) || !strides_ok(p->v_stride, eb) ||
+      !strides_ok(p->o_stride, eb) || !strides_ok(p->do_stride, eb) || !lse_strides_ok(p->lse_stride) ||
+      !strides_ok(p->dq_stride, eb) || !strides_ok(p->dk_stride, eb) || !strides_ok(p->dv_stride, eb))
     return FA_ERR_ALIGN;
   // every input is read through buffer resources with 32-bit byte offsets inside one
   // (batch, head) slice; dq, dk and dv are written through 64-bit addresses
   const int L = p->seqlen, D = p->head_dim;
-  if (!slice_fits(p->q_stride, L, D, 2) || !slice_fits(p->do_stride, L, D, 2) || !slice_fits(p->o_stride, L, D, 2) ||
-      !slice_fits(p->lse_stride, L, 1, 4) || !slice_fits(p->k_stride, L, D, 2) || !slice_fits(p->v_stride, L, D, 2))
+  if (!slice_fits(p->q_stride, L, D, eb) || !slice_fits(p->do_stride, L, D, eb) || !slice_fits(p->o_stride, L, D, eb) ||
+      !slice_fits(p->lse_stride, L, 1, 4) || !slice_fits(p->k_stride, L, D, eb) || !slice_fits(p->v_stride, L, D, eb))
     return FA_ERR_OVERFLOW;
   return FA_OK;
 }
@@ -248,6 +284,8 @@ int run_fwd(const fa_fwd_params* p, const float* sinks, void* stream, const int3
   copy3(a.so_out, p->o_stride);
   copy3(a.slse, p->lse_stride);
   if (cu_seqlens) set_varlen(&a, cu_seqlens, total_rows);
+  if (p->dtype == FA_DTYPE_F32)
+    return fa::launch_fwd_f32(a, p->head_dim, static_cast<hipStream_t>(stream)) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
   int hpw, wh, wq;
   choose_qmajor(a.G, p->head_dim <= 64 ? 2 : 1, &hpw, &wh, &wq);
   a.wh = wh;
@@ -326,7 +364,7 @@ int fa_fwd_varlen(const fa_fwd_params* p, const int32_t* cu_seqlens, int32_t tot
   if (rc != FA_OK) return rc;
   // rows outside every sequence: o = 0, lse = -inf (an empty row)
   fa::TailArgs t = tail_args(cu_seqlens, p->batch, total_rows);
-  tail_add(&t, p->o, p->o_stride, p->heads_q, p->head_dim, 2, 0u);
+  tail_add(&t, p->o, p->o_stride, p->heads_q, p->head_dim, elem_bytes(p->dtype), 0u);
   tail_add(&t, p->lse, p->lse_stride, p->heads_q, 1, 4, 0xff800000u);
   return fa::launch_varlen_tail(t, static_cast<hipStream_t>(stream)) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
@@ -359,9 +397,8 @@ size_t fa_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t heads_kv, 
                               int32_t head_dim, int32_t window, int32_t sink) {
   if (check_common(batch, heads_q, heads_kv, seqlen, head_dim, window, sink, 1.f, FA_DTYPE_BF16) != FA_OK)
     return 0;
-  const SinkPlan sp = sink_plan(seqlen, window, sink);
-  return delta_bytes(batch, heads_q, seqlen) + partial_bytes(batch, heads_kv, head_dim, sp) +
-         dsink_part_bytes(batch, heads_q, seqlen) + dq_sink_slot_bytes(batch, heads_q, heads_kv, seqlen, head_dim, sp);
+  return delta_bytes(batch, heads_q, seqlen) + dsink_part_bytes(batch, heads_q, seqlen) +
+         partial_region_bytes(batch, heads_q, heads_kv, seqlen, head_dim, window, sink);
 }
 
 }  // extern "C"
@@ -404,14 +441,23 @@ int prepare_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
   a.wq = wq;
   a.n_qtiles = (a.L + 32 * wq - 1) / (32 * wq);
 
-  const SinkPlan sp = sink_plan(a.L, p->window, p->sink);
+  // workspace: row statistics | learned-sink partials | partial region (see partial_region_bytes)
   char* ws = static_cast<char*>(workspace);
-  a.partial = reinterpret_cast<float*>(ws + delta_bytes(a.B, a.Hq, a.L));
-  const size_t off_dsink = delta_bytes(a.B, a.Hq, a.L) + partial_bytes(a.B, a.Hkv, p->head_dim, sp);
+  const size_t off_dsink = delta_bytes(a.B, a.Hq, a.L);
   a.dsink_part = reinterpret_cast<float*>(ws + off_dsink);
-  const size_t off_dq_slots = off_dsink + dsink_part_bytes(a.B, a.Hq, a.L);
+  a.partial = reinterpret_cast<float*>(ws + off_dsink + dsink_part_bytes(a.B, a.Hq, a.L));
+  if (p->dtype == FA_DTYPE_F32) {
+    const F32Plan fp = f32_plan(a.L, p->window, p->sink);
+    a.n_kblocks = fp.n_kt;
+    a.nsp = fp.nsp;
+    a.n_chunks = fp.n_chunks;
+    a.chunk_rows = kF32ChunkRows;
+    *out = a;
+    return FA_OK;
+  }
+  const SinkPlan sp = sink_plan(a.L, p->window, p->sink);
   a.sink_dq = sp.dq;
-  if (sp.dq) a.dq_sink_part = reinterpret_cast<float*>(ws + off_dq_slots);
+  if (sp.dq) a.dq_sink_part = a.partial + partial_bytes(a.B, a.Hkv, p->head_dim, sp) / sizeof(float);
   a.n_kblocks = (a.L + fa::kKvKeys - 1) / fa::kKvKeys;
   a.nsp = sp.nsp;
   a.n_chunks = sp.n_chunks;
@@ -423,11 +469,15 @@ int prepare_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
 }
 
 int run_dq(const fa::Args& a, const fa_bwd_params* p, int hpw, hipStream_t s) {
-  return fa::launch_bwd_dq(a, p->dtype, p->head_dim, hpw, s) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+  const hipError_t e = p->dtype == FA_DTYPE_F32 ? fa::launch_bwd_dq_f32(a, p->head_dim, s)
+                                                : fa::launch_bwd_dq(a, p->dtype, p->head_dim, hpw, s);
+  return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 
 int run_dkdv(const fa::Args& a, const fa_bwd_params* p, hipStream_t s) {
-  return fa::launch_bwd_dkdv(a, p->dtype, p->head_dim, s) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+  const hipError_t e = p->dtype == FA_DTYPE_F32 ? fa::launch_bwd_dkdv_f32(a, p->head_dim, s)
+                                                : fa::launch_bwd_dkdv(a, p->dtype, p->head_dim, s);
+  return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 
 }  // namespace
@@ -479,9 +529,10 @@ int fa_bwd_varlen(const fa_bwd_params* p, const int32_t* cu_seqlens, int32_t tot
   if (r != FA_OK) return r;
   // rows outside every sequence have zero gradients
   fa::TailArgs t = tail_args(cu_seqlens, p->batch, total_rows);
-  tail_add(&t, p->dq, p->dq_stride, p->heads_q, p->head_dim, 2, 0u);
-  tail_add(&t, p->dk, p->dk_stride, p->heads_kv, p->head_dim, 2, 0u);
-  tail_add(&t, p->dv, p->dv_stride, p->heads_kv, p->head_dim, 2, 0u);
+  const int eb = elem_bytes(p->dtype);
+  tail_add(&t, p->dq, p->dq_stride, p->heads_q, p->head_dim, eb, 0u);
+  tail_add(&t, p->dk, p->dk_stride, p->heads_kv, p->head_dim, eb, 0u);
+  tail_add(&t, p->dv, p->dv_stride, p->heads_kv, p->head_dim, eb, 0u);
   return fa::launch_varlen_tail(t, s) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 
@@ -505,7 +556,7 @@ const char* fa_strerror(int status) {
     case FA_ERR_NULL: return "a required pointer is NULL";
     case FA_ERR_SHAPE: return "invalid shape: batch, heads and seqlen must be >= 1 and heads_q % heads_kv == 0";
     case FA_ERR_HEAD_DIM: return "head_dim must be one of 16, 32, 64, 128 (64 or 128 for fa_fwd_fp8*)";
-    case FA_ERR_DTYPE: return "dtype must be FA_DTYPE_BF16 or FA_DTYPE_F16 (FA_DTYPE_FP8_E4M3 for fa_fwd_fp8*)";
+    case FA_ERR_DTYPE: return "dtype must be FA_DTYPE_BF16, FA_DTYPE_F16 or FA_DTYPE_F32 (FA_DTYPE_FP8_E4M3 for fa_fwd_fp8*)";
     case FA_ERR_ALIGN: return "tensors must be 16-byte aligned with non-negative strides that are multiples of 16 bytes (lse: 4-byte aligned, non-negative strides)";
     case FA_ERR_MASK: return "window < 1 and sink < 1 leave every query row fully masked";
     case FA_ERR_WORKSPACE: return "workspace is NULL, not 256-byte aligned or smaller than fa_bwd_workspace_bytes()";

@@ -194,6 +194,22 @@ __device__ __forceinline__ float buf_ldf(rsrc_t r, uint32_t off) {
 __device__ __forceinline__ void buf_dma16(rsrc_t r, uint16_t* lds_dst, uint32_t off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds_dst), 16, off, 0, 0, 0);
 }
+// LDS DMA of 4 bytes per lane (buffer_load_dword ... lds): lane l's word lands at lds_dst + 4 l.
+__device__ __forceinline__ void buf_dma4(rsrc_t r, uint16_t* lds_dst, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds_dst), 4, off, 0, 0, 0);
+}
+// s_waitcnt immediate (gfx9 encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
+// that waits until at most `vm` vector-memory loads of the wave are outstanding and every LDS
+// operation has completed; exports are not waited for.
+constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | (((vm >> 4) & 3) << 14) | (7 << 4); }
+// That wait, then the workgroup barrier.  Inline assembly, so that the compiler neither drops nor
+// relaxes the wait: it does not track the LDS writes of DMA loads.
+template <int VM>
+__device__ __forceinline__ void wait_vm_lgkm0_barrier() {
+  static_assert(VM >= 0 && VM <= 63, "vmcnt range");
+  asm volatile("s_waitcnt %0\n\ts_barrier" ::"n"(waitcnt_vm_lgkm0(VM)) : "memory");
+}
+
 // Bytes spanned by `rows` fp32 values with stride `stride` (0 if none).
 __device__ __forceinline__ uint32_t span_f32(int rows, int64_t stride) {
   return rows > 0 ? uint32_t((int64_t(rows - 1) * stride + 1) * 4) : 0u;

@@ -25,8 +25,9 @@ namespace {
 int32_t dtype_code(const at::Tensor& t) {
   if (t.scalar_type() == at::kBFloat16) return FA_DTYPE_BF16;
   if (t.scalar_type() == at::kHalf) return FA_DTYPE_F16;
+  if (t.scalar_type() == at::kFloat) return FA_DTYPE_F32;
   throw std::invalid_argument("q has dtype " + std::string(c10::toString(t.scalar_type())) +
-                              "; supported dtypes are bfloat16 and float16");
+                              "; supported dtypes are bfloat16, float16 and float32");
 }
 
 void check(const std::vector<std::pair<const at::Tensor*, const char*>>& ts) {
@@ -45,12 +46,13 @@ void check(const std::vector<std::pair<const at::Tensor*, const char*>>& ts) {
   }
 }
 
-// Inputs the kernels cannot read directly (head-dim stride != 1, strides not multiples of 8
-// elements, base not 16-byte aligned) are copied to a contiguous layout first.
+// Inputs the kernels cannot read directly (head-dim stride != 1, strides not whole multiples of
+// 16 bytes, base not 16-byte aligned) are copied to a contiguous layout first.
 at::Tensor kernel_ready(const at::Tensor& t) {
   const auto st = t.strides();
+  const int64_t m = 16 / int64_t(t.element_size()) - 1;
   const auto misaligned = [&](const at::Tensor& x) { return (reinterpret_cast<uintptr_t>(x.data_ptr()) & 15) != 0; };
-  if (st[3] != 1 || (st[0] & 7) || (st[1] & 7) || (st[2] & 7) || misaligned(t)) {
+  if (st[3] != 1 || (st[0] & m) || (st[1] & m) || (st[2] & m) || misaligned(t)) {
     at::Tensor c = t.contiguous();
     if (misaligned(c)) c = c.clone(at::MemoryFormat::Contiguous);
     return c;

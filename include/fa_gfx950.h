@@ -41,8 +41,11 @@ extern "C" {
 #define FA_GFX950_VERSION 10400 /* 1.4.0 */
 
 /* Element types of q/k/v/o/dout/dq/dk/dv.  All of them share one type per call, except in
- * fa_fwd_fp8 and fa_fwd_fp8_pv: FA_DTYPE_FP8_E4M3 means OCP float8 e4m3 q, k, v and a bf16 o. */
-enum fa_dtype { FA_DTYPE_BF16 = 1, FA_DTYPE_F16 = 2, FA_DTYPE_FP8_E4M3 = 3 };
+ * fa_fwd_fp8 and fa_fwd_fp8_pv: FA_DTYPE_FP8_E4M3 means OCP float8 e4m3 q, k, v and a bf16 o.
+ * FA_DTYPE_F32: float32 tensors, computed in float32 throughout (every product on the fp32
+ * matrix instruction, P and dS kept in float32), as the reference accepts float32 q/k/v
+ * (flash_attention_gpt_oss.py:356-357; benchmark_backward_speed.py:35-36). */
+enum fa_dtype { FA_DTYPE_BF16 = 1, FA_DTYPE_F16 = 2, FA_DTYPE_FP8_E4M3 = 3, FA_DTYPE_F32 = 4 };
 
 enum fa_status {
   FA_OK = 0,
@@ -51,8 +54,8 @@ enum fa_status {
   FA_ERR_HEAD_DIM = -3,    /* D not in {16, 32, 64, 128} */
   FA_ERR_DTYPE = -4,       /* dtype not an fa_dtype */
   FA_ERR_ALIGN = -5,       /* a tensor's base not 16-byte aligned, or a stride negative or not a
-                              multiple of 16 bytes (8 16-bit or 16 e4m3 elements); lse not 4-byte
-                              aligned */
+                              multiple of 16 bytes (8 16-bit, 4 float32 or 16 e4m3 elements); lse
+                              not 4-byte aligned */
   FA_ERR_MASK = -6,        /* window < 1 and sink < 1: every query row would be fully masked */
   FA_ERR_WORKSPACE = -7,   /* workspace NULL or smaller than fa_bwd_workspace_bytes() */
   FA_ERR_LAUNCH = -8,      /* a HIP launch failed */

@@ -118,6 +118,10 @@ def _bwd_params(**over):
     ({"head_dim": 8}, _lib.FA_ERR_HEAD_DIM),
     ({"dtype": 0}, _lib.FA_ERR_DTYPE),
     ({"dtype": 3}, _lib.FA_ERR_DTYPE),
+    ({"dtype": 5}, _lib.FA_ERR_DTYPE),
+    ({"dtype": _lib.FA_DTYPE_F32}, _lib.FA_OK),
+    ({"dtype": _lib.FA_DTYPE_F32, "q_stride": (8 * 128 * 68, 128 * 68, 68)}, _lib.FA_OK),  # 68 floats: 272 B
+    ({"dtype": _lib.FA_DTYPE_F32, "q_stride": (8 * 128 * 66, 128 * 66, 66)}, _lib.FA_ERR_ALIGN),  # 264 B
     ({"window": 0, "sink": 0}, _lib.FA_ERR_MASK),
     ({"window": -5, "sink": 0}, _lib.FA_ERR_MASK),
     ({"q": (1 << 20) + 8}, _lib.FA_ERR_ALIGN),
@@ -233,12 +237,13 @@ def test_entry_points_reject_before_any_hip_call():
 def test_workspace_bytes():
     L = _lib.lib()
     ws = L.fa_bwd_workspace_bytes
-    # delta: B*Hq*round_up(L, 32) floats, 256-aligned; no sink split when every row is within
-    # the window of the sink block; the learned-sink partials: B*Hq*ceil(L/32) floats, 256-aligned
-    assert ws(1, 8, 2, 128, 64, 200, 4) == 8 * 128 * 4 + 256
-    assert ws(1, 8, 2, 100, 64, 200, 4) == 8 * 128 * 4 + 256
+    # row statistics (lse * log2(e) and -delta): 2 * B*Hq*round_up(L, 32) floats, 256-aligned; no
+    # sink split when every row is within the window of the sink block; the learned-sink partials:
+    # B*Hq*ceil(L/32) floats, 256-aligned
+    assert ws(1, 8, 2, 128, 64, 200, 4) == 2 * 8 * 128 * 4 + 256
+    assert ws(1, 8, 2, 100, 64, 200, 4) == 2 * 8 * 128 * 4 + 256
     L_, D = 4096, 64
-    expect_delta = 64 * 4096 * 4
+    expect_delta = 2 * 64 * 4096 * 4
     expect_dsink = 64 * (4096 // 32) * 4
     # S <= 16 sink keys, rows past block 0's window (row 191): the dK/dV kernel keeps one slot
     # (block 0's own rows) per KV head, dK and dV, S = 4 rows x D fp32; the dQ kernel's slots are
@@ -318,3 +323,17 @@ def test_scratch_entry_point_rejects_before_any_hip_call():
     assert L.fa_check_bwd(ctypes.byref(p)) == _lib.FA_OK
     assert L.fa_bwd_workspace_bytes(1, 64, 8, big, 64, 16, 4) > _lib.FA_SCRATCH_BYTES
     assert L.fa_bwd_scratch(ctypes.byref(p), None) == _lib.FA_ERR_SCRATCH
+
+
+def test_float32_slices_are_bounded_with_4_byte_elements():
+    """A float32 head slice spans twice the bytes of a 16-bit one: the 2^31-byte bound of the
+    kernels' 32-bit offsets is reached at half the rows."""
+    L = _lib.lib()
+    F32 = _lib.FA_DTYPE_F32
+    rows = (1 << 31) // (64 * 4)  # rows of 64 floats in 2^31 bytes: one too many
+    st = (rows * 64, rows * 64, 64)
+    assert L.fa_check_fwd(ctypes.byref(_fwd_params(dtype=F32, seqlen=rows - 1, q_stride=st, k_stride=st,
+                                                   v_stride=st))) == _lib.FA_OK
+    assert L.fa_check_fwd(ctypes.byref(_fwd_params(dtype=F32, seqlen=rows, q_stride=st))) == _lib.FA_ERR_OVERFLOW
+    assert L.fa_check_fwd(ctypes.byref(_fwd_params(dtype=_lib.FA_DTYPE_BF16, seqlen=rows, q_stride=st))) == \
+        _lib.FA_OK

@@ -240,7 +240,7 @@ def test_error_behaviour_on_gpu(gpu):
     with pytest.raises(AssertionError, match="only causal"):
         fa.flash_swda_with_sink(q, k, v, 8, 1, is_causal=False)
     with pytest.raises(ValueError, match="dtype"):
-        fa.flash_swda_with_sink(q.float(), k.float(), v.float(), 8, 1)
+        fa.flash_swda_with_sink(q.double(), k.double(), v.double(), 8, 1)
     q48, k48, v48, _ = make_inputs(1, 4, 2, 64, 48, BF, seed=1)
     with pytest.raises(ValueError, match="head_dim"):
         fa.flash_swda_with_sink(q48, k48, v48, 8, 1)
