@@ -303,7 +303,13 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // resident workgroup per CU needs.
   constexpr bool kStash = F8 || D <= 64;
   constexpr int STASH = kStash ? HPW * KS * 512 : 0;  // per wave: the next tile's Q fragments
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF + 4 * STASH + 2 * kPatterns * kPatternFloats];
+  // Small head dims (16-bit D <= 32): a block's compute is short next to the latency of fetching
+  // the next block, so every block of a tile (up to NBUF at a time) is fetched at once, by LDS DMA,
+  // into NBUF buffers, and the blocks are then computed back to back.  Wider heads double-buffer
+  // through registers, one block ahead.
+  constexpr bool PRE = !F8 && D <= 32;
+  constexpr int NBUF = PRE ? 32768 / (2 * BUF) : 2;  // 32 KiB of K/V blocks
+  __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF * BUF + 4 * STASH + 2 * kPatterns * kPatternFloats];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -353,7 +359,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // of lane l at 16 bytes each, in lane order -- so they occupy no registers while the current
   // tile computes.  Buffer resources over the sequence's rows [0, L) of the head: rows past L
   // read as zero.
-  uint16_t* stash = lds + 2 * BUF + wave * STASH;
+  uint16_t* stash = lds + NBUF * BUF + wave * STASH;
   auto q_rsrc = [&](const TileIdx& t, int h) {
     KArgs& A = args_fresh();
     return make_rsrc(reinterpret_cast<const char*>(A.q) + EB * slice_off(A.sq, t.b, t.hw + h, t.row),
@@ -388,7 +394,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   const uint32_t bk = uint32_t(EB * a.sk[2]), bv = uint32_t(EB * a.sv[2]);  // bytes per key row
 
   // the recurring masks (made visible by the barrier before the first key block)
-  float* const pat = reinterpret_cast<float*>(lds + 2 * BUF + 4 * STASH);
+  float* const pat = reinterpret_cast<float*>(lds + NBUF * BUF + 4 * STASH);
   fwd_patterns(pat, W, S);
   const EdgeOffsets eo = edge_offsets(W);
 
@@ -477,39 +483,76 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     }
   };
 
-  if (plan.nb > 0) {  // (a tile past its sequence's end, in a variable-length batch, has none)
-    gload(qplan_block(plan, 0));
-    sstore(0);
-    __syncthreads();
-  }
-
-  for (int i = 0; i < plan.nb; ++i) {
-    const int kb = qplan_block(plan, i);
-    const bool more = i + 1 < plan.nb;
-    if (more) gload(qplan_block(plan, i + 1));
-    // the next tile's Q rows into the stash, once this tile's have been read out of it
-    if (kStash && i == 0 && tile + wgs_x < t_hi) {
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      stash_rows(decode(tile + wgs_x));
-    }
-    if (wave_active) {
-      const uint16_t* Kl = lds + (i & 1) * BUF;
-      const uint16_t* Vl = Kl + KBUF;
-      if constexpr (F8 == 2) {
-        const bool need[2] = {wave_needs(kb, qw, L, W, S), wave_needs(kb + 32, qw, L, W, S)};
-        if (need[0] || need[1]) fwd_block_pv8<D, HPW>(a, Kl, Vl, kb, need, qw, q, qf, m2, lacc, acc, pat, eo);
-      } else {
+  // one key block [kb, kb + 64) from LDS buffer `buf`
+  auto compute_block = [&](int kb, int buf) {
+    if (!wave_active) return;
+    const uint16_t* Kl = lds + buf * BUF;
+    const uint16_t* Vl = Kl + KBUF;
+    if constexpr (F8 == 2) {
+      const bool need[2] = {wave_needs(kb, qw, L, W, S), wave_needs(kb + 32, qw, L, W, S)};
+      if (need[0] || need[1]) fwd_block_pv8<D, HPW>(a, Kl, Vl, kb, need, qw, q, qf, m2, lacc, acc, pat, eo);
+    } else {
 #pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-          const int ks0 = kb + 32 * sb;
-          if (!wave_needs(ks0, qw, L, W, S)) continue;
-          fwd_half<E, D, HPW, F8>(a, Kl + 32 * sb * (KBUF / BN), Vl + 32 * sb * D, ks0, qw, q, qf, m2, lsum, acc,
-                                  pat, eo);
-        }
+      for (int sb = 0; sb < 2; ++sb) {
+        const int ks0 = kb + 32 * sb;
+        if (!wave_needs(ks0, qw, L, W, S)) continue;
+        fwd_half<E, D, HPW, F8>(a, Kl + 32 * sb * (KBUF / BN), Vl + 32 * sb * D, ks0, qw, q, qf, m2, lsum, acc,
+                                pat, eo);
       }
     }
-    if (more) sstore((i + 1) & 1);
-    __syncthreads();
+  };
+
+  if constexpr (PRE) {
+    // DMA of a 64-key block into buffer j: the block's K and V tiles are CPB 16-byte chunks each,
+    // 2 CPB / 64 instructions of 64 lanes; wave w issues instructions [w NIW, (w + 1) NIW), and lane
+    // l of instruction p (of K or V) loads the chunk that the swizzle places at position 64 p + l
+    constexpr int IPT = CPB / 64;       // instructions per tile (K or V)
+    constexpr int NIW = 2 * IPT / 4;    // per wave
+    static_assert(NIW >= 1 && 2 * IPT == 4 * NIW, "whole instructions per wave");
+    auto dma_block = [&](int kb, int j) {
+#pragma unroll
+      for (int n = 0; n < NIW; ++n) {
+        const int ii = wave * NIW + n, is_v = ii >= IPT, pi = is_v ? ii - IPT : ii;
+        const int pos = 64 * pi + lane, row = pos / CPR, col = (pos % CPR) ^ swz<D>(row);
+        uint16_t* dst = lds + j * BUF + (is_v ? KBUF : 0) + 512 * pi;
+        const uint32_t off = uint32_t(int64_t(kb + row) * (is_v ? bv : bk)) + 16u * uint32_t(col);
+        if (is_v) buf_dma16(rv, dst, off);
+        else buf_dma16(rk, dst, off);
+      }
+    };
+    for (int g0 = 0; g0 < plan.nb; g0 += NBUF) {
+      const int ng = min(NBUF, plan.nb - g0);
+      for (int j = 0; j < ng; ++j) dma_block(qplan_block(plan, g0 + j), j);
+      // the next tile's Q rows into the stash, once this tile's have been read out of it
+      const bool stash_now = kStash && g0 == 0 && tile + wgs_x < t_hi;
+      if (stash_now) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        stash_rows(decode(tile + wgs_x));
+        wait_vm_lgkm0_barrier<HPW * KS>();  // the blocks have landed (the stash may be in flight)
+      } else {
+        wait_vm_lgkm0_barrier<0>();
+      }
+      for (int j = 0; j < ng; ++j) compute_block(qplan_block(plan, g0 + j), j);
+      __syncthreads();  // before the buffers are refilled
+    }
+  } else {
+    if (plan.nb > 0) {  // (a tile past its sequence's end, in a variable-length batch, has none)
+      gload(qplan_block(plan, 0));
+      sstore(0);
+      __syncthreads();
+    }
+    for (int i = 0; i < plan.nb; ++i) {
+      const bool more = i + 1 < plan.nb;
+      if (more) gload(qplan_block(plan, i + 1));
+      // the next tile's Q rows into the stash, once this tile's have been read out of it
+      if (kStash && i == 0 && tile + wgs_x < t_hi) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        stash_rows(decode(tile + wgs_x));
+      }
+      compute_block(qplan_block(plan, i), i & 1);
+      if (more) sstore((i + 1) & 1);
+      __syncthreads();
+    }
   }
   if (kStash && plan.nb == 0 && tile + wgs_x < t_hi) {  // no key block: stash it here
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
