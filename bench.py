@@ -178,6 +178,28 @@ def profile_launches(cfg, q, k, v, do, n):
     print(f"profile_launches: {n} x copy {COPY_BYTES} B, fwd, bwd_dq, bwd_dkdv on {cfg['name']}", flush=True)
 
 
+def warm_clocks(fa, cfg, q, k, v, do, seconds):
+    """Untimed fwd+bwd steps for about `seconds` (synchronising every 50 steps to read the clock);
+    returns how many ran."""
+    import torch
+
+    qg, kg, vg = (t.detach().clone().requires_grad_() for t in (q, k, v))
+
+    def steps(m):
+        for _ in range(m):
+            qg.grad = kg.grad = vg.grad = None
+            fa.flash_swda_with_sink(qg, kg, vg, cfg["W"], cfg["S"]).backward(do)
+        torch.cuda.synchronize()
+
+    steps(2)  # first calls: library and code-object loading, allocator growth
+    n = 2
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        steps(50)
+        n += 50
+    return n
+
+
 def time_steps(fa, cfg, q, k, v, do, steps, warmup):
     import torch
 
@@ -513,6 +535,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--clock-warm-s", type=float, default=0.2,
+                    help="seconds of untimed fwd+bwd steps that bring the GPU to its working clocks first")
     ap.add_argument("--cpu-baseline-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sdpa-baseline", action="store_true")
@@ -545,9 +569,11 @@ def main():
     acct = kernel_accounting(cfg)
     wl = _mod("flops").Workload(cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"], cfg["D"], cfg["W"], cfg["S"])
 
-    # The per-kernel timing runs first: its few hundred launches also bring the GPU's clocks to
-    # their working level before the warm-up and timed steps (with only a handful of warm-up
-    # steps on a cold GPU, the timed steps would otherwise run partly at idle clocks).
+    # A GPU coming out of idle takes about 200 back-to-back steps (some 30 ms) to reach its working
+    # clocks: measured from a cold start, c2 steps time 127 us at first and settle at 110 us.  So
+    # the GPU first runs fwd+bwd steps for clock_warm_s before anything is timed (the per-kernel
+    # timing, then the W untimed warm-up steps and the K timed ones).
+    warm_steps = warm_clocks(fa, cfg, q, k, v, do, args.clock_warm_s)
     kus = time_kernels(cfg, q, k, v, do, iters=args.kernel_iters)
     t = time_steps(fa, cfg, q, k, v, do, args.steps, args.warmup)
 
@@ -603,6 +629,7 @@ def main():
         "fwdbwd_median_ms": round(t["fwdbwd_median_ms"], 4),
         "peak_mem_gb": round(t["peak_mem_gb"], 4),
         "fwdbwd_roofline_frac": round(wl.roofline_seconds("fwdbwd") / (t["fwdbwd_ms"] * 1e-3), 4),
+        "clock_warm_steps": warm_steps,
         "kernels": kernels,
         "roofline": roofline,
     }

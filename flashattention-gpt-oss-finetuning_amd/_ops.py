@@ -161,6 +161,16 @@ def _binding():
 _BINDING = False
 
 
+def autograd_binding(t: torch.Tensor):
+    """The C++ binding when it is built and `t` is a GPU tensor, else None.  Its autograd functions
+    (swda, swda_sinks) run the forward's bookkeeping and the whole backward in C++, which saves
+    tens of microseconds of host time per training step; tensors that are not on a GPU go through
+    the Python autograd functions, which raise for them."""
+    if not t.is_cuda:
+        return None
+    return _binding()
+
+
 def forward(q, k, v, window: int, sink: int, scale: float, sinks=None):
     """Returns (o, lse) for q [B,Hq,L,D], k/v [B,Hkv,L,D]; `sinks` ([Hq] learned sink logits or
     None) selects fa_fwd_sinks.  o has q's memory layout."""

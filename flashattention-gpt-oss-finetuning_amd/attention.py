@@ -179,16 +179,39 @@ def _check_shapes(q, k, v):
         raise AssertionError("Number of query heads must be divisible by number of K/V heads")
 
 
+def _swda(q, k, v, window_size, sink_size, is_causal=True, scale=None, sinks=None):
+    """FlashSWDAWithSink (or, with `sinks`, FlashSWDAWithLearnedSinks) applied to GPU tensors
+    through the binding's autograd functions in C++ (fa_torch.swda / swda_sinks): the same checks
+    and messages, the same kernels, saved tensors and gradients, without Python in the backward.
+    Without the binding, or for tensors that are not on a GPU, the Python autograd functions."""
+    b = _ops.autograd_binding(q)
+    if b is None:
+        if sinks is None:
+            return FlashSWDAWithSink.apply(q, k, v, window_size, sink_size, is_causal, scale)
+        return FlashSWDAWithLearnedSinks.apply(q, k, v, sinks, window_size, sink_size, scale)
+    if not is_causal:
+        raise AssertionError("Currently, only causal attention is supported")
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    _check_shapes(q, k, v)
+    if sinks is None:
+        return b.swda(q, k, v, int(window_size), int(sink_size), float(scale))
+    if window_size is None:
+        window_size = q.shape[2]
+    return b.swda_sinks(q, k, v, sinks, int(window_size), int(sink_size), float(scale))
+
+
 def flash_swda_with_sink(q, k, v, window_size: int, sink_size: int = 0, is_causal: bool = True,
                          scale: Optional[float] = None):
-    """Functional form, flash_attention_gpt_oss.py:437-438."""
-    return FlashSWDAWithSink.apply(q, k, v, window_size, sink_size, is_causal, scale)
+    """Functional form, flash_attention_gpt_oss.py:437-438 (FlashSWDAWithSink.apply; on GPU
+    tensors its C++ twin, see _swda)."""
+    return _swda(q, k, v, window_size, sink_size, is_causal, scale)
 
 
 def swa_sink_attention(q, k, v, window_size: int, sink_size: int):
     """Registry form ``func(q, k, v, window_size, sink_size) -> o`` with the default scale 1/sqrt(D)
     (triton_attention, benchmark_backward_speed.py:615-622): one backward call, fa_bwd."""
-    return FlashSWDAWithSink.apply(q, k, v, window_size, sink_size, True, None)
+    return _swda(q, k, v, window_size, sink_size, True, None)
 
 
 class FlashSWDAWithSinkSplit(torch.autograd.Function):

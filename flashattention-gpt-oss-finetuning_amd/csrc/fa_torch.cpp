@@ -5,7 +5,8 @@
 // launch -- in C++, so a forward + backward costs a few microseconds of host time instead of
 // the tens that per-field ctypes marshalling takes.  Every FLOP still runs in libfa_gfx950.so;
 // this module only calls fa_fwd / fa_bwd / fa_fwd_sinks / fa_bwd_sinks / fa_bwd_workspace_bytes /
-// fa_strerror.
+// fa_strerror.  swda / swda_sinks are the autograd functions themselves in C++ (forward, saved
+// tensors, backward), which the functional forms of the Python package call.
 //
 // Error behaviour matches the ctypes path (_ops.py): tensors not on a GPU -> RuntimeError,
 // unsupported dtype or shape -> ValueError, a C ABI status -> ValueError (argument) or
@@ -190,9 +191,72 @@ std::vector<at::Tensor> bwd(const at::Tensor& q_in, const at::Tensor& k_in, cons
   return {dq, dk, dv};
 }
 
+// The autograd function of flash_attention_gpt_oss.py:340-438 (FlashSWDAWithSink) in C++: the
+// forward saves (q, k, v, o, lse) and the window / sink / scale, the backward returns dq, dk, dv
+// and no gradient for the other four arguments.  The autograd engine runs this backward on its
+// device thread without taking the Python interpreter lock, so a training step spends no Python
+// time in the backward; the computation is the same fa_fwd / fa_bwd calls as fwd() / bwd().
+struct SwdaFunction : public torch::autograd::Function<SwdaFunction> {
+  static at::Tensor forward(torch::autograd::AutogradContext* ctx, const at::Tensor& q, const at::Tensor& k,
+                            const at::Tensor& v, int64_t window, int64_t sink, double scale) {
+    std::vector<at::Tensor> r = fwd(q, k, v, window, sink, scale, c10::nullopt);
+    ctx->save_for_backward({q, k, v, r[0], r[1]});
+    ctx->saved_data["window"] = window;
+    ctx->saved_data["sink"] = sink;
+    ctx->saved_data["scale"] = scale;
+    return r[0];
+  }
+
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    const torch::autograd::variable_list s = ctx->get_saved_variables();
+    std::vector<at::Tensor> g = bwd(s[0], s[1], s[2], s[3], s[4], grads[0], ctx->saved_data["window"].toInt(),
+                                    ctx->saved_data["sink"].toInt(), ctx->saved_data["scale"].toDouble(), c10::nullopt);
+    return {g[0], g[1], g[2], at::Tensor(), at::Tensor(), at::Tensor()};
+  }
+};
+
+// The same with GPT-OSS learned sink logits (sinks [Hq]): the backward also returns d sinks, in
+// the dtype of sinks.
+struct SwdaSinksFunction : public torch::autograd::Function<SwdaSinksFunction> {
+  static at::Tensor forward(torch::autograd::AutogradContext* ctx, const at::Tensor& q, const at::Tensor& k,
+                            const at::Tensor& v, const at::Tensor& sinks, int64_t window, int64_t sink, double scale) {
+    std::vector<at::Tensor> r = fwd(q, k, v, window, sink, scale, sinks);
+    ctx->save_for_backward({q, k, v, r[0], r[1], sinks});
+    ctx->saved_data["window"] = window;
+    ctx->saved_data["sink"] = sink;
+    ctx->saved_data["scale"] = scale;
+    return r[0];
+  }
+
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    const torch::autograd::variable_list s = ctx->get_saved_variables();
+    std::vector<at::Tensor> g = bwd(s[0], s[1], s[2], s[3], s[4], grads[0], ctx->saved_data["window"].toInt(),
+                                    ctx->saved_data["sink"].toInt(), ctx->saved_data["scale"].toDouble(), s[5]);
+    return {g[0], g[1], g[2], g[3].to(s[5].scalar_type()), at::Tensor(), at::Tensor(), at::Tensor()};
+  }
+};
+
+at::Tensor swda(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, int64_t window, int64_t sink,
+                double scale) {
+  return SwdaFunction::apply(q, k, v, window, sink, scale);
+}
+
+at::Tensor swda_sinks(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& sinks,
+                      int64_t window, int64_t sink, double scale) {
+  return SwdaSinksFunction::apply(q, k, v, sinks, window, sink, scale);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("swda", &swda,
+        "autograd forward of causal sliding-window + sink attention: (q, k, v, window, sink, scale) -> o",
+        py::arg("q"), py::arg("k"), py::arg("v"), py::arg("window"), py::arg("sink"), py::arg("scale"));
+  m.def("swda_sinks", &swda_sinks,
+        "autograd forward with learned sink logits: (q, k, v, sinks, window, sink, scale) -> o", py::arg("q"),
+        py::arg("k"), py::arg("v"), py::arg("sinks"), py::arg("window"), py::arg("sink"), py::arg("scale"));
   m.doc() = "PyTorch binding of libfa_gfx950.so (fa_fwd / fa_bwd)";
   m.def("fwd", &fwd, "forward: (q, k, v, window, sink, scale, sinks=None) -> (o, lse)", py::arg("q"), py::arg("k"),
         py::arg("v"), py::arg("window"), py::arg("sink"), py::arg("scale"), py::arg("sinks") = py::none());

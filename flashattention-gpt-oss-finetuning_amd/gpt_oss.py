@@ -21,7 +21,7 @@ from typing import Optional
 
 import torch
 
-from .attention import FlashSWDAWithLearnedSinks, FlashSWDAWithSink, flash_swda_with_sink_varlen
+from .attention import _swda, flash_swda_with_sink_varlen
 
 
 class _BatchFacts:
@@ -91,10 +91,7 @@ def attention(q, k, v, window_size: Optional[int] = None, sink_size: int = 0, si
     if layout == "blhd":
         q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
     W = q.shape[2] if window_size is None else int(window_size)
-    if sinks is None:
-        o = FlashSWDAWithSink.apply(q, k, v, W, sink_size, True, scale)
-    else:
-        o = FlashSWDAWithLearnedSinks.apply(q, k, v, sinks, W, sink_size, scale)
+    o = _swda(q, k, v, W, sink_size, True, scale, sinks=sinks)
     return o.transpose(1, 2) if layout == "blhd" else o
 
 

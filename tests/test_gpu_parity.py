@@ -221,6 +221,34 @@ def test_autograd_path_and_noncontiguous_inputs(gpu):
     assert torch.equal(qv.grad, dq2) and torch.equal(kv_.grad, dk2) and torch.equal(vv.grad, dv2)
 
 
+@pytest.mark.parametrize("learned", [False, True], ids=["positional", "learned_sinks"])
+def test_functional_forms_use_the_cxx_autograd_function(gpu, learned):
+    """On GPU tensors flash_swda_with_sink / attention run the binding's C++ autograd functions
+    (no Python backward node); outputs and every gradient equal the Python autograd functions'
+    (FlashSWDAWithSink / FlashSWDAWithLearnedSinks) bit for bit."""
+    fa = load_pkg()
+    B, Hq, Hkv, L, D, W, S = 2, 8, 2, 200, 64, 48, 4
+    q, k, v, do = make_inputs(B, Hq, Hkv, L, D, BF, seed=11)
+    sinks = (torch.linspace(-1.0, 2.0, Hq, device="cuda") if learned else None)
+    runs = []
+    for cxx in (True, False):
+        qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+        sg = sinks.clone().requires_grad_() if learned else None
+        if cxx:
+            o = fa.attention(qg, kg, vg, W, S, sinks=sg) if learned else fa.flash_swda_with_sink(qg, kg, vg, W, S)
+            assert not isinstance(o.grad_fn, torch.autograd.function.BackwardCFunction)
+        elif learned:
+            o = fa.FlashSWDAWithLearnedSinks.apply(qg, kg, vg, sg, W, S, None)
+        else:
+            o = fa.FlashSWDAWithSink.apply(qg, kg, vg, W, S, True, None)
+        if not cxx:
+            assert isinstance(o.grad_fn, torch.autograd.function.BackwardCFunction)
+        o.backward(do)
+        runs.append([o, qg.grad, kg.grad, vg.grad] + ([sg.grad] if learned else []))
+    for a, b in zip(*runs):
+        assert a.dtype == b.dtype and torch.equal(a, b)
+
+
 def test_backward_is_deterministic(gpu):
     ops = load_mod("_ops")
     q, k, v, do = make_inputs(1, 16, 2, 2048, 64, BF, seed=9)
