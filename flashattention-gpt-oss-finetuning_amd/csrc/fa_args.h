@@ -54,6 +54,13 @@ struct Args {
   int sink_dq;       // 1 in that mode
   float* dq_sink_part;  // [n_tiles][dK, dV][srows][D] fp32: a run's sums at the slot of its first tile
   int dq_wgs;           // the dQ kernel's grid (set for the sink fold)
+  // The sliding dQ kernel (fa_bwd_slide.hip), when it runs instead of bwd_dq_kernel (dq_slide = 1):
+  // its workgroups ("units") take slide_ct consecutive 32-row tiles of 8 query heads; a (batch, KV
+  // head, head group of 8) has slide_ncu units, in that order (chunks fastest).  In dq_sink_mode
+  // unit u writes slot u of dq_sink_part.
+  int dq_slide;
+  int slide_ct;
+  int slide_ncu;
   // variable-length batches: NULL, or [B + 1] device offsets of the sequences' first rows in
   // tensors of total_rows packed rows (L is then the longest sequence, batch strides are 0)
   const int* cu_seqlens;
@@ -121,6 +128,8 @@ hipError_t launch_fwd(const Args& a, int dtype, int D, int hpw, hipStream_t stre
 // e4m3 q, k, v; bf16 o; fp8_pv: P V on the fp8 MFMA as well
 hipError_t launch_fwd_fp8(const Args& a, int D, int hpw, bool fp8_pv, hipStream_t stream);
 hipError_t launch_bwd_dq(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
+// the sliding dQ kernel (D = 64, 16-bit, G a multiple of 8, 1 <= W <= 161, S <= 32)
+hipError_t launch_bwd_dq_slide(const Args& a, int dtype, hipStream_t stream);
 hipError_t launch_bwd_dkdv(const Args& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_bwd_sink_logits(const Args& a, hipStream_t stream);  // after launch_bwd_dq
 hipError_t launch_varlen_tail(const TailArgs& t, hipStream_t stream);

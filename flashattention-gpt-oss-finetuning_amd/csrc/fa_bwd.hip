@@ -462,7 +462,23 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
 // ---------------------------------------------------------------------------------------------
 // Adds up the sink keys' dK/dV partials (defined with bwd_sink_fold_kernel below).
 template <typename E, int D>
-__device__ void fold_sink_keys(int b, int kvh, int nk, const Seq& sq);
+__device__ void fold_sink_keys(int b, int kvh, int nk, const Seq& sq, float* smem);
+
+// 16-bit elements of the dK/dV kernel's LDS: NSTG stages of two items (Q and dO tiles, 32 rows,
+// and 128 elements of row statistics each), or the fp32 partials of the head-slot sum if larger.
+__host__ __device__ constexpr int dkdv_lds_elems(int D) {
+  const int stages = (D == 128 ? 3 : 4) * 2 * (2 * 32 * D + 128);
+  const int red = 2 * 2 * 2 * (D >= 32 ? D / 32 : 1) * 16 * 64;
+  return stages > red ? stages : red;
+}
+
+// Does key block 0's workgroup fold the sink keys itself (dq_sink_mode; the sink keys' (key,
+// column) pairs fit one pass of 256 threads; the dQ kernel's run list and the chunk sums fit the
+// kernel's LDS)?  Otherwise bwd_sink_fold_kernel does it after the dK/dV kernel.
+__host__ __device__ inline bool dkdv_folds_in_kernel(const Args& a, int D) {
+  return a.sink_dq && (a.S < kKvKeys ? a.S : kKvKeys) * D <= 256 &&
+         ((a.dq_wgs + 3) & ~3) + 4 * 256 <= dkdv_lds_elems(D) / 2;
+}
 
 // D = 16 keeps four waves per SIMD (at most 128 VGPRs); the wider head dims need more registers.
 template <typename E, int D>
@@ -474,9 +490,7 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   constexpr int STAGE = 2 * SLOT;            // two items per step
   constexpr int NSTG = D == 128 ? 3 : 4;     // LDS stages: see the staging below
   constexpr int CPR = D / 8;                 // 16-byte chunks per row
-  constexpr int RED = 2 * 2 * DB * 16 * 64;  // fp32 partials of the two hh = 1 waves
-  constexpr int LDS_ELEMS = (NSTG * STAGE > 2 * RED) ? NSTG * STAGE : 2 * RED;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[dkdv_lds_elems(D)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -697,12 +711,14 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
     int cp = 0, cur = 0, nxt = NSTG - 1;  // stage of step s, stage of step s + NSTG - 1
     for (int s = 0; s < n_steps; ++s) {
       wait_vm_lgkm0_barrier<(NSTG - 2) * PER>();  // step s landed everywhere
-      issue(nxt);
+      // (D = 128 issues after its compute: measured 4% faster there, slower at D = 64)
+      if constexpr (D != 128) issue(nxt);
       if (needed(cp)) {
         f32x16 sacc, dpacc;
         scores(cur, sacc, dpacc);
         finish(cur, cp, sacc, dpacc);
       }
+      if constexpr (D == 128) issue(nxt);
       cp = cp + 1 == n_qp ? 0 : cp + 1;
       cur = cur + 1 == NSTG ? 0 : cur + 1;
       nxt = nxt + 1 == NSTG ? 0 : nxt + 1;
@@ -775,11 +791,11 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   }
 
   // dq_sink_mode with at most 256 (sink key, column) pairs: key block 0's workgroup folds its
-  // sink keys (see fold_sink_keys), one pair per thread; the barrier makes its own slot writes
-  // visible to all its threads.
-  if (a.sink_dq && partial_block && !is_chunk && min(S, kKvKeys) * D <= 256) {
+  // sink keys (see fold_sink_keys); the barrier makes its own slot writes visible to all its
+  // threads, and every thread is past its last read of the LDS that the fold reuses.
+  if (partial_block && !is_chunk && dkdv_folds_in_kernel(a, D)) {
     __syncthreads();
-    fold_sink_keys<E, D>(b, kvh, min(min(S, kKvKeys), L), sq);
+    fold_sink_keys<E, D>(b, kvh, min(min(S, kKvKeys), L), sq, reinterpret_cast<float*>(lds));
   }
 }
 
@@ -794,8 +810,7 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
 // then visible without a device-wide fence).  In dq_sink_mode the dQ kernel's slots are complete
 // before the dK/dV kernel starts and the only other partial is that of key block 0's own
 // workgroup, so when the sink keys' (key, column) pairs fit one pass of 256 threads that
-// workgroup folds them itself after writing its slot (fold_sink_keys, one pair per thread, the
-// slots in the same order) and no fold launch follows.
+// workgroup folds them itself after writing its slot (fold_sink_keys) and no fold launch follows.
 // ---------------------------------------------------------------------------------------------
 template <typename E, int D>
 __device__ void fold_sink_key(int b, int kvh, int key, const Seq& sq, float (&part)[2][256 / D][D]) {
@@ -826,7 +841,29 @@ __device__ void fold_sink_key(int b, int kvh, int key, const Seq& sq, float (&pa
       sv += xv[j];
     }
   }
-  if (Ak.sink_dq) {
+  if (Ak.sink_dq && Ak.dq_slide) {
+    // the sliding dQ kernel's units of (b, KV head) that own tiles, in (head group, chunk) order
+    const int hgn = Ak.G / 8, ncu = Ak.slide_ncu;
+    const int nv = min(ncu, ((sq.L + 31) / 32 + Ak.slide_ct - 1) / Ak.slide_ct);
+    const int base = (kvh * Ak.B + b) * hgn * ncu, n = hgn * nv;
+    const int n_out = 2 * Ak.srows * D;
+    const float* dsrc = Ak.dq_sink_part + row * D + d;
+    for (int j0 = g; j0 < n; j0 += NG * kBatch) {
+      float xk[kBatch], xv[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int jj = j0 + j * NG, i = jj < n ? jj : 0;
+        const float* p = dsrc + int64_t(base + (i / nv) * ncu + i % nv) * n_out;
+        xk[j] = jj < n ? p[0] : 0.f;
+        xv[j] = jj < n ? p[Ak.srows * D] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        sk += xk[j];
+        sv += xv[j];
+      }
+    }
+  } else if (Ak.sink_dq) {
     // The dQ kernel's flushed partials of this (b, KV head) = tiles [(b + B kvh) tpk, + tpk): on
     // XCD x, whose tiles are [x_lo, x_hi) and whose Ak.dq_wgs / 8 workgroups stride through them,
     // the runs start at the first Ak.dq_wgs / 8 tiles of [max(x_lo, lo), min(x_hi, hi)).  All the
@@ -877,48 +914,98 @@ __device__ void fold_sink_key(int b, int kvh, int key, const Seq& sq, float (&pa
   __syncthreads();  // part is free again
 }
 
+// fold_sink_keys: the same sums for all nk sink keys at once, in key block 0's workgroup.  A slot's
+// 2 nk D values (dK rows, then dV rows) are C = nk D / 2 chunks of four floats; thread t < P C
+// (P = 256 / C >= 2 slot groups) takes chunk t % C of the slots at positions j, j + P, j + 2P, ...
+// (j = t / C) of the list [own slot, the dQ kernel's run slots in (XCD, tile) order], kBatch
+// 16-byte loads in flight at a time; the P group sums of a chunk are then added in LDS in order
+// j = 0, 1, ....  `smem` is the kernel's LDS, free at this point (dq_wgs run indices, then the P C
+// chunk sums).
 template <typename E, int D>
-__device__ void fold_sink_keys(int b, int kvh, int nk, const Seq& sq) {
+__device__ void fold_sink_keys(int b, int kvh, int nk, const Seq& sq, float* smem) {
   KArgs& Ak = args_fresh();
-  constexpr int kBatch = 16;
-  const int t = threadIdx.x, key = t / D, d = t % D;
-  if (key >= nk) return;
-  const int64_t slot_stride = int64_t(2) * Ak.srows * D;
-  const int64_t blk = int64_t(b * Ak.Hkv + kvh) * Ak.nsp;  // key block 0
-  const float* own = Ak.partial + blk * (Ak.n_chunks + 1) * slot_stride + key * D + d;
-  float sk = own[0], sv = own[Ak.srows * D];
-  // the dQ kernel's runs of this (b, KV head), in (XCD, tile) order as in fold_sink_key
-  constexpr int nx = 8;
-  const int tpk = Ak.n_qtiles * (Ak.G / Ak.wh);
-  const int n_tiles = tpk * Ak.B * Ak.Hkv;
-  const int wgs_x = Ak.dq_wgs / nx;
-  const int lo = (b + Ak.B * kvh) * tpk, hi = lo + tpk;
-  const int per = n_tiles / nx, rem = n_tiles % nx;
-  const int n_out = 2 * Ak.srows * D;
-  const float* dsrc = Ak.dq_sink_part + key * D + d;
-  for (int x = 0; x < nx; ++x) {
-    const int x_lo = x * per + min(x, rem), x_hi = x_lo + per + (x < rem ? 1 : 0);
-    const int r_lo = max(x_lo, lo), r_hi = min(x_hi, hi);
-    const int n = r_hi > r_lo ? min(wgs_x, r_hi - r_lo) : 0;
-    for (int j0 = 0; j0 < n; j0 += kBatch) {
-      float xk[kBatch], xv[kBatch];
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int jj = j0 + j;
-        const float* p = dsrc + int64_t(r_lo + (jj < n ? jj : 0)) * n_out;
-        xk[j] = jj < n ? p[0] : 0.f;
-        xv[j] = jj < n ? p[Ak.srows * D] : 0.f;
-      }
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        sk += xk[j];
-        sv += xv[j];
-      }
+  constexpr int kBatch = D <= 32 ? 8 : 32;  // 4 kBatch registers per thread (D <= 32: <= 128 in all)
+  const int t = threadIdx.x;
+  const int Q = nk * D / 4;  // chunks per half
+  const int C = 2 * Q;
+  const int P = 256 / C;
+  const int srd = Ak.srows * D;  // floats of a half slot
+  const int64_t slot_stride = int64_t(2) * srd;
+  // the run slots of this (b, KV head): on XCD x, whose tiles are [x_lo, x_hi) and whose
+  // Ak.dq_wgs / 8 workgroups stride through them, the runs start at the first Ak.dq_wgs / 8 tiles
+  // of [max(x_lo, lo), min(x_hi, hi)) (see the dQ kernel's flush)
+  int* runs = reinterpret_cast<int*>(smem);
+  float* red = smem + ((Ak.dq_wgs + 3) & ~3);
+  int nr = 0;
+  if (Ak.dq_slide) {
+    // the sliding dQ kernel's units of (b, KV head) that own tiles, in (head group, chunk) order
+    const int hgn = Ak.G / 8, ncu = Ak.slide_ncu;
+    const int nv = min(ncu, ((sq.L + 31) / 32 + Ak.slide_ct - 1) / Ak.slide_ct);
+    const int base = (kvh * Ak.B + b) * hgn * ncu;
+    nr = hgn * nv;
+    for (int i = t; i < nr; i += 256) runs[i] = base + (i / nv) * ncu + i % nv;
+  } else {
+    constexpr int nx = 8;
+    const int tpk = Ak.n_qtiles * (Ak.G / Ak.wh);
+    const int n_tiles = tpk * Ak.B * Ak.Hkv;
+    const int wgs_x = Ak.dq_wgs / nx;
+    const int lo = (b + Ak.B * kvh) * tpk, hi = lo + tpk;
+    const int per = n_tiles / nx, rem = n_tiles % nx;
+    for (int x = 0; x < nx; ++x) {
+      const int x_lo = x * per + min(x, rem), x_hi = x_lo + per + (x < rem ? 1 : 0);
+      const int r_lo = max(x_lo, lo), r_hi = min(x_hi, hi);
+      const int n = r_hi > r_lo ? min(wgs_x, r_hi - r_lo) : 0;
+      for (int i = t; i < n; i += 256) runs[nr + i] = r_lo + i;
+      nr += n;
     }
   }
-  const uint32_t pk = E::pack2(sk * Ak.scale, sv);
-  reinterpret_cast<uint16_t*>(Ak.dk)[slice_off(Ak.sdk, b, kvh, sq.row + key) + d] = uint16_t(pk);
-  reinterpret_cast<uint16_t*>(Ak.dv)[slice_off(Ak.sdv, b, kvh, sq.row + key) + d] = uint16_t(pk >> 16);
+  __syncthreads();
+  const int c = t % C, j = t / C;
+  const int off = c < Q ? 4 * c : srd + 4 * (c - Q);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (j < P) {
+    if (j == 0) {  // the workgroup's own slot (key block 0) comes first
+      const int64_t blk = int64_t(b * Ak.Hkv + kvh) * Ak.nsp;
+      acc = *reinterpret_cast<const f32x4*>(Ak.partial + blk * (Ak.n_chunks + 1) * slot_stride + off);
+    }
+    const float* dsrc = Ak.dq_sink_part + off;
+    for (int i0 = j; i0 < nr; i0 += P * kBatch) {
+      f32x4 x[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int i = i0 + u * P;
+        x[u] = *reinterpret_cast<const f32x4*>(dsrc + int64_t(runs[i < nr ? i : 0]) * slot_stride);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if (i0 + u * P < nr) {
+          acc[0] += x[u][0];
+          acc[1] += x[u][1];
+          acc[2] += x[u][2];
+          acc[3] += x[u][3];
+        }
+      }
+    }
+    *reinterpret_cast<f32x4*>(red + 4 * (j * C + c)) = acc;
+  }
+  __syncthreads();
+  if (t < C) {
+    f32x4 tot = *reinterpret_cast<const f32x4*>(red + 4 * t);
+    for (int g = 1; g < P; ++g) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(red + 4 * (g * C + t));
+      tot[0] += v[0];
+      tot[1] += v[1];
+      tot[2] += v[2];
+      tot[3] += v[3];
+    }
+    const bool is_dk = t < Q;
+    const int e = 4 * (is_dk ? t : t - Q), key = e / D, col = e % D;
+    const float m = is_dk ? Ak.scale : 1.f;
+    const u32x2 out = {E::pack2(tot[0] * m, tot[1] * m), E::pack2(tot[2] * m, tot[3] * m)};
+    char* base = reinterpret_cast<char*>(is_dk ? Ak.dk : Ak.dv);
+    const int64_t at = is_dk ? slice_off(Ak.sdk, b, kvh, sq.row + key) : slice_off(Ak.sdv, b, kvh, sq.row + key);
+    *reinterpret_cast<u32x2*>(base + 2 * (at + col)) = out;
+  }
 }
 
 template <typename E, int D>
@@ -1051,11 +1138,12 @@ template <typename E, int D>
 static hipError_t launch_dkdv_d(const Args& a, hipStream_t stream) {
   const dim3 grid(a.n_chunk_wgs + a.B * a.Hkv * a.n_kblocks), block(256);
   Args ad = a;
-  if (a.sink_dq) ad.dq_wgs = dq_grid<E, D, true>(a);  // the in-kernel fold finds the dQ slots by it
+  // the in-kernel fold finds the dQ slots by the dQ grid (and sizes its run list in LDS by it)
+  if (a.sink_dq) ad.dq_wgs = a.dq_slide ? (a.G / 8) * a.slide_ncu : dq_grid<E, D, true>(a);
   hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), grid, block, 0, stream, ad);
   hipError_t e = hipGetLastError();
-  // dq_sink_mode with at most 256 (sink key, column) pairs folds inside the dK/dV kernel
-  if (e != hipSuccess || a.nsp == 0 || (a.sink_dq && min(a.S, kKvKeys) * D <= 256)) return e;
+  // the sink keys are folded inside the dK/dV kernel (dkdv_folds_in_kernel) or by a launch of their own
+  if (e != hipSuccess || a.nsp == 0 || dkdv_folds_in_kernel(ad, D)) return e;
   const int64_t n = int64_t(a.B) * a.Hkv * min(a.S, kKvKeys * a.nsp);  // one workgroup per sink key
   hipLaunchKernelGGL((bwd_sink_fold_kernel<E, D>), dim3(unsigned(n)), block, 0, stream, ad);
   return hipGetLastError();

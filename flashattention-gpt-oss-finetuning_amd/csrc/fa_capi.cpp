@@ -156,6 +156,31 @@ void copy3(int64_t dst[3], const int64_t src[3]) {
   for (int i = 0; i < 3; ++i) dst[i] = src[i];
 }
 
+// Compute units of the current device (256 on MI355X; 256 if the query fails).
+int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n < 1)
+    n = 256;
+  return n;
+}
+
+// The sliding dQ kernel (fa_bwd_slide.hip) serves D = 64 16-bit backwards whose KV groups hold a
+// multiple of 8 query heads, with a window of 1..161 keys (at most 6 key halves of 32 in LDS) and
+// at most 32 sink keys (one sink half).  Its workgroups take slide_ct consecutive 32-row tiles,
+// sized so that the units about fill the device once.
+void plan_slide(fa::Args& a, int D) {
+  if (D != 64 || a.G % 8 != 0 || a.W < 1 || a.W > fa::kSlideMaxW || a.S > 32 || a.L < 1) return;
+  const int64_t n_qt = (int64_t(a.L) + 31) / 32;
+  const int64_t groups = int64_t(a.B) * a.Hkv * (a.G / 8);
+  const int64_t cus = device_cus();
+  int64_t ct = (groups * n_qt + cus - 1) / cus;
+  if (ct < 1) ct = 1;
+  a.dq_slide = 1;
+  a.slide_ct = int(ct);
+  a.slide_ncu = int((n_qt + ct - 1) / ct);
+}
+
 fa::Args base_args(int32_t B, int32_t Hq, int32_t Hkv, int32_t L, int32_t D, int32_t W, int32_t S,
                    float scale) {
   fa::Args a;
@@ -464,13 +489,15 @@ int prepare_bwd(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
   a.chunk_rows = kChunkRows;
   a.srows = sp.srows;
   a.n_chunk_wgs = a.B * a.Hkv * a.nsp * a.n_chunks;
+  plan_slide(a, p->head_dim);
   *out = a;
   return FA_OK;
 }
 
 int run_dq(const fa::Args& a, const fa_bwd_params* p, int hpw, hipStream_t s) {
   const hipError_t e = p->dtype == FA_DTYPE_F32 ? fa::launch_bwd_dq_f32(a, p->head_dim, s)
-                                                : fa::launch_bwd_dq(a, p->dtype, p->head_dim, hpw, s);
+                       : a.dq_slide         ? fa::launch_bwd_dq_slide(a, p->dtype, s)
+                                            : fa::launch_bwd_dq(a, p->dtype, p->head_dim, hpw, s);
   return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 

@@ -67,6 +67,24 @@ FA_HD bool tile_full(int ks0, int qr, int W, int S) {
   return (ks0 + 31 <= qr) && ((qr + 31 - ks0 < W) || (ks0 + 32 <= S));
 }
 
+// ---- the sliding dQ kernel (fa_bwd_slide.hip) --------------------------------------------------
+// A workgroup walks consecutive 32-row tiles; tile m (rows [32m, 32m + 32)) visits the 32-key
+// window halves slide_hlo(m, W) .. m (those with wave_needs) and, when slide_sink_half(m, W, S),
+// the sink half (keys [0, 32)) before them.  Half j lives in ring slot j % kSlideRing; tile m's
+// halves span at most kSlideRing - 1 consecutive indices (W <= kSlideMaxW), so the slot of half
+// m + 1, loaded during tile m, is not one that tile m reads.
+constexpr int kSlideRing = 7;
+constexpr int kSlideMaxW = 32 * (kSlideRing - 2) + 1;  // 161
+
+// First window half of tile m: the half holding key 32m - W + 1 (clamped to 0); W >= 1.
+FA_HD int slide_hlo(int m, int W) {
+  const int back = (W - 1 + 31) / 32;  // ceil((W - 1) / 32)
+  return m > back ? m - back : 0;
+}
+
+// Does tile m visit the sink half separately (it holds sink keys and is not a window half)?
+FA_HD bool slide_sink_half(int m, int W, int S) { return S > 0 && slide_hlo(m, W) > 0; }
+
 // ---- key-major kernel (dK, dV) ----------------------------------------------------------------
 // A workgroup owns the kKvKeys keys [kKvKeys*kblk, +kKvKeys); each of its waves owns a 32-key
 // half.  The rows that can see a 32-key half [ks0, ks0 + 32) through the window are

@@ -1,7 +1,7 @@
 // plan_check.cpp - host check of the kernels' visit plan (csrc/fa_plan.h compiled with g++).
 //
-// Walks the loops of the query-major kernels (fa_fwd.hip fwd_kernel, fa_bwd.hip bwd_dq_kernel)
-// and of the key-major kernel (bwd_dkdv_kernel) over many (L, W, S, rows-per-workgroup,
+// Walks the loops of the query-major kernels (fa_fwd.hip fwd_kernel, fa_bwd.hip bwd_dq_kernel,
+// fa_bwd_slide.hip bwd_dq_slide_kernel) and of the key-major kernel (bwd_dkdv_kernel) over many (L, W, S, rows-per-workgroup,
 // chunk size) cases and checks that
 //   * every allowed (q, k) pair is visited exactly once and no other pair is counted,
 //   * a tile reported "full" (mask skipped) holds only allowed pairs,
@@ -57,6 +57,43 @@ static int check_qmajor(int L, int W, int S, int wq) {
     for (int k = 0; k < L; ++k) {
       const int want = ref_allowed(q, k, W, S) ? 1 : 0;
       if (cnt[size_t(q) * L + k] != want) return fail("q-major visit count", L, W, S, wq, q, k, cnt[size_t(q) * L + k]);
+    }
+  return 0;
+}
+
+// The sliding dQ kernel (1 <= W <= kSlideMaxW, S <= 32): 32-row tiles, each visiting the sink half
+// (when slide_sink_half) and then the window halves slide_hlo .. m that wave_needs.  Also checks
+// that a tile's halves span at most kSlideRing - 1 indices (the ring slot of half m + 1 is free
+// during tile m) and that, in dq_sink_mode, every tile with rows past dq_sink_row0 visits the sink
+// half (where the kernel accumulates the sink keys' dK/dV).
+static int check_slide(int L, int W, int S) {
+  std::vector<int> cnt(size_t(L) * L, 0);
+  for (int m = 0; 32 * m < L; ++m) {
+    const int qw = 32 * m, hlo = slide_hlo(m, W);
+    if (m - hlo > kSlideRing - 2) return fail("slide window spans too many halves", L, W, S, m, qw, hlo, 0);
+    if (dq_sink_mode(L, W, S) && qw + 31 >= dq_sink_row0(L, W) && !slide_sink_half(m, W, S))
+      return fail("slide sink rows without the sink half", L, W, S, m, qw, 0, 0);
+    auto visit = [&](int ks0) {
+      const bool full = tile_full(ks0, qw, W, S);
+      for (int r = 0; r < 32; ++r)
+        for (int c = 0; c < 32; ++c) {
+          const int q = qw + r, k = ks0 + c;
+          if (q >= L) continue;
+          const bool ok = full || allowed(q - k, k, W, S);
+          if (full && !(k < L && ref_allowed(q, k, W, S))) return fail("slide full half has a masked pair", L, W, S, m, q, k, 0);
+          if (ok && k >= L) return fail("slide key beyond L passes the mask", L, W, S, m, q, k, 0);
+          if (ok) ++cnt[size_t(q) * L + k];
+        }
+      return 0;
+    };
+    if (slide_sink_half(m, W, S) && visit(0)) return 1;
+    for (int j = hlo; j <= m; ++j)
+      if (wave_needs(32 * j, qw, L, W, S) && visit(32 * j)) return 1;
+  }
+  for (int q = 0; q < L; ++q)
+    for (int k = 0; k < L; ++k) {
+      const int want = ref_allowed(q, k, W, S) ? 1 : 0;
+      if (cnt[size_t(q) * L + k] != want) return fail("slide visit count", L, W, S, 0, q, k, cnt[size_t(q) * L + k]);
     }
   return 0;
 }
@@ -135,7 +172,7 @@ static int check_kvmajor(int L, int W, int S, int chunk_rows) {
 
 int main() {
   const int Ls[] = {1, 2, 5, 31, 32, 33, 63, 64, 65, 100, 127, 128, 129, 200, 257, 300, 513};
-  const int Ws[] = {0, 1, 2, 5, 31, 32, 33, 64, 100, 128, 129, 256, 100000};
+  const int Ws[] = {0, 1, 2, 5, 31, 32, 33, 64, 100, 128, 129, 160, 161, 162, 256, 100000};
   const int Ss[] = {0, 1, 4, 16, 31, 32, 33, 64, 65, 100, 100000};
   long cases = 0;
   for (int L : Ls)
@@ -149,6 +186,10 @@ int main() {
         }
         for (int cr : {32, 64, 256}) {
           if (check_kvmajor(L, W, S, cr)) return 1;
+          ++cases;
+        }
+        if (W >= 1 && W <= kSlideMaxW && S <= 32) {
+          if (check_slide(L, W, S)) return 1;
           ++cases;
         }
       }
