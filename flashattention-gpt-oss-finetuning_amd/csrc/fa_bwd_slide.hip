@@ -122,18 +122,28 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
   const int sink_row0 = dq_sink_row0(L, W);
   uint16_t* const ptile = stash + 2 * TILE;  // P / dS of the sink keys, in the O tile (read for delta only)
 
-  // ---- prologue: the first tile's rows, its window halves and the sink half
+  // ---- prologue: the first tile's rows and the sink half (used first), then its window halves,
+  // which may still be in flight while the first tile reads its rows and computes the sink half
   stash_rows(qt0);
   float lse_next = load_lse(qt0);
-  for (int j = slide_hlo(qt0, W); j <= qt0; ++j) load_half(j, j % kRing);
   if (S > 0) load_half(0, kRing);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  const int hlo0 = slide_hlo(qt0, W);
+  for (int j = hlo0; j <= qt0; ++j) load_half(j, j % kRing);
+  switch (qt0 - hlo0 + 1) {  // window halves issued last: wait for everything before them
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+  }
 
   for (int qt = qt0; qt < qt1; ++qt) {
     const int qw = 32 * qt, q = qw + r32;
     const bool has_next = qt + 1 < qt1;
-    // every wave's loads for this tile have landed (each waited for its own before its stores)
-    __syncthreads();
+    // every wave's loads for this tile have landed (each waited for its own before its stores;
+    // in the first tile, all but the window halves)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     // the next tile's diagonal half, into the slot this tile does not use
     if (has_next) load_half(qt + 1, (qt + 1) % kRing);
 
@@ -153,20 +163,6 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
     const float delta = sum_halves(dsum);
     const float ndelta = -delta;
     const float lse2 = q < L ? lse_next * kLog2e : __builtin_inff();
-    {
-      KArgs& A = args_fresh();
-      if (hf == 0) {
-        float* st = A.delta + ((int64_t(b) * A.Hq + h) * (A.Lp / 32) + qt) * 64;
-        st[r32] = lse2;
-        st[32 + r32] = ndelta;
-      }
-      if (A.sink_logits) {
-        float v = q < L ? fast_exp2(A.sink_logits[h] * kLog2e - lse2) * delta : 0.f;
-#pragma unroll
-        for (int mm = 16; mm >= 1; mm >>= 1) v += __shfl_xor(v, mm);
-        if (lane == 0) A.dsink_part[(int64_t(b) * A.Hq + h) * (A.Lp / 32) + qt] = -v;
-      }
-    }
 
     f32x16 acc[DB];
 #pragma unroll
@@ -276,7 +272,28 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
         }
       }
     }
+    if (qt == qt0) {
+      // the first tile's window halves (every wave's share): only the next tile's half, issued at
+      // the top of this tile, may still be in flight
+      if (has_next) wait_vm_lgkm0_barrier<1>();
+      else wait_vm_lgkm0_barrier<0>();
+    }
     refill();
+    {
+      // the row statistics for the dK/dV kernel (stored here, after the first tile's wait above)
+      KArgs& A = args_fresh();
+      if (hf == 0) {
+        float* st = A.delta + ((int64_t(b) * A.Hq + h) * (A.Lp / 32) + qt) * 64;
+        st[r32] = lse2;
+        st[32 + r32] = ndelta;
+      }
+      if (A.sink_logits) {
+        float v = q < L ? fast_exp2(A.sink_logits[h] * kLog2e - lse2) * delta : 0.f;
+#pragma unroll
+        for (int mm = 16; mm >= 1; mm >>= 1) v += __shfl_xor(v, mm);
+        if (lane == 0) A.dsink_part[(int64_t(b) * A.Hq + h) * (A.Lp / 32) + qt] = -v;
+      }
+    }
     // the window halves
     for (int j = hlo; j <= qt; ++j) {
       if (!wave_needs(32 * j, qw, L, W, S)) continue;
