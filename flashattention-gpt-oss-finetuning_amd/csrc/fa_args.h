@@ -54,10 +54,11 @@ struct Args {
   int sink_dq;       // 1 in that mode
   float* dq_sink_part;  // [n_tiles][dK, dV][srows][D] fp32: a run's sums at the slot of its first tile
   int dq_wgs;           // the dQ kernel's grid (set for the sink fold)
-  // The sliding dQ kernel (fa_bwd_slide.hip), when it runs instead of bwd_dq_kernel (dq_slide = 1):
-  // its workgroups ("units") take slide_ct consecutive 32-row tiles of 8 query heads; a (batch, KV
-  // head, head group of 8) has slide_ncu units, in that order (chunks fastest).  In dq_sink_mode
-  // unit u writes slot u of dq_sink_part.
+  // The sliding dQ kernel (fa_bwd_slide.hip), when it runs instead of bwd_dq_kernel (dq_slide = 1),
+  // and the sliding forward (fa_fwd.hip fwd_slide_kernel): their workgroups ("units") take slide_ct
+  // consecutive 32-row tiles of 8 query heads; a (batch, KV head, head group of 8) has slide_ncu
+  // units, in that order (chunks fastest).  In dq_sink_mode dQ unit u writes slot u of
+  // dq_sink_part.
   int dq_slide;
   int slide_ct;
   int slide_ncu;
@@ -130,6 +131,8 @@ hipError_t launch_fwd_fp8(const Args& a, int D, int hpw, bool fp8_pv, hipStream_
 hipError_t launch_bwd_dq(const Args& a, int dtype, int D, int hpw, hipStream_t stream);
 // the sliding dQ kernel (D = 64, 16-bit, G a multiple of 8, 1 <= W <= 161, S <= 32)
 hipError_t launch_bwd_dq_slide(const Args& a, int dtype, hipStream_t stream);
+// the sliding forward (the same, W <= 129; reads slide_ct / slide_ncu)
+hipError_t launch_fwd_slide(const Args& a, int dtype, hipStream_t stream);
 hipError_t launch_bwd_dkdv(const Args& a, int dtype, int D, hipStream_t stream);
 hipError_t launch_bwd_sink_logits(const Args& a, hipStream_t stream);  // after launch_bwd_dq
 hipError_t launch_varlen_tail(const TailArgs& t, hipStream_t stream);

@@ -181,6 +181,22 @@ void plan_slide(fa::Args& a, int D) {
   a.slide_ncu = int((n_qt + ct - 1) / ct);
 }
 
+// The sliding forward (fa_fwd.hip fwd_slide_kernel): the same shapes with W <= 129; two
+// workgroups per CU.  Returns whether it applies (then slide_ct / slide_ncu are set).
+bool plan_fwd_slide(fa::Args& a, int D, int dtype) {
+  if (dtype == FA_DTYPE_F32 || D != 64 || a.G % 8 != 0 || a.W < 1 || a.W > fa::kFwdSlideMaxW || a.S > 32 ||
+      a.L < 1)
+    return false;
+  const int64_t n_qt = (int64_t(a.L) + 31) / 32;
+  const int64_t groups = int64_t(a.B) * a.Hkv * (a.G / 8);
+  const int64_t slots = 2 * int64_t(device_cus());
+  int64_t ct = (groups * n_qt + slots - 1) / slots;
+  if (ct < 1) ct = 1;
+  a.slide_ct = int(ct);
+  a.slide_ncu = int((n_qt + ct - 1) / ct);
+  return true;
+}
+
 fa::Args base_args(int32_t B, int32_t Hq, int32_t Hkv, int32_t L, int32_t D, int32_t W, int32_t S,
                    float scale) {
   fa::Args a;
@@ -311,6 +327,8 @@ int run_fwd(const fa_fwd_params* p, const float* sinks, void* stream, const int3
   if (cu_seqlens) set_varlen(&a, cu_seqlens, total_rows);
   if (p->dtype == FA_DTYPE_F32)
     return fa::launch_fwd_f32(a, p->head_dim, static_cast<hipStream_t>(stream)) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+  if (plan_fwd_slide(a, p->head_dim, p->dtype))
+    return fa::launch_fwd_slide(a, p->dtype, static_cast<hipStream_t>(stream)) == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
   int hpw, wh, wq;
   choose_qmajor(a.G, p->head_dim <= 64 ? 2 : 1, &hpw, &wh, &wq);
   a.wh = wh;

@@ -612,6 +612,173 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   }  // tiles
 }
 
+// ---------------------------------------------------------------------------------------------
+// Sliding forward, for the GPT-OSS sliding layers (16-bit, D = 64, KV groups of a multiple of 8
+// query heads, 1 <= W <= 129, S <= 32; the C ABI's plan_fwd_slide checks): the forward twin of
+// bwd_dq_slide_kernel (fa_bwd_slide.hip).  A workgroup is 4 waves x 2 heads -- the 8 query heads
+// of one head group -- and walks slide_ct consecutive 32-row tiles.  Tile m visits the sink half
+// (when slide_sink_half) and the window halves slide_hlo(m, W) .. m, all resident in an LDS ring
+// of kFwdSlideRing slots (half j in slot j % kFwdSlideRing) plus a sink slot; tile m brings in one
+// half, the next tile's diagonal half m + 1, by LDS DMA into the slot that its own halves
+// m - 4 .. m leave free.  The next tile's Q rows are loaded into registers while the current tile
+// computes.  LDS: 7 slots of K and V (8 KB each) and the mask patterns = 72 KB, two workgroups per
+// CU.  The per-half work is fwd_half, the same as fwd_kernel's.
+// ---------------------------------------------------------------------------------------------
+template <typename E>
+__global__ __launch_bounds__(256, 2) void fwd_slide_kernel(const Args a) {
+  constexpr int D = 64, HPW = 2, KS = D / 16, DB = D / 32;
+  constexpr int TILE = 32 * D;    // one swizzled [32][D] tile of 16-bit values
+  constexpr int HALF = 2 * TILE;  // a ring slot: K, then V, of 32 keys
+  constexpr int NR = kFwdSlideRing;
+  constexpr int CPR = D / 8;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[(NR + 1) * HALF + 2 * kPatterns * kPatternFloats];
+  uint16_t* const ring = lds;
+  float* const pat = reinterpret_cast<float*>(lds + (NR + 1) * HALF);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r32 = lane & 31, hf = lane >> 5;
+  const int W = a.W, S = a.S;
+
+  // unit -> (KV head, batch, head group, chunk), chunks fastest (as bwd_dq_slide_kernel)
+  const int hg_n = a.G / 8;
+  const int unit = xcd_remap(blockIdx.x, gridDim.x);
+  const int chunk = unit % a.slide_ncu;
+  const int rest = unit / a.slide_ncu;
+  const int hg = rest % hg_n;
+  const int bk = rest / hg_n;
+  const int b = bk % a.B, kvh = bk / a.B;
+  const Seq sq = seq_of(a, b);
+  const int L = sq.L;
+  const int n_qt = (L + 31) / 32;
+  const int qt0 = chunk * a.slide_ct;
+  const int qt1 = min(qt0 + a.slide_ct, n_qt);
+  if (qt0 >= qt1) return;  // past the end of a short sequence (variable-length batches)
+  const int hw = kvh * a.G + hg * 8 + HPW * wave;  // this wave's first query head
+
+  // the recurring masks (visible after the first barrier)
+  fwd_patterns(pat, W, S);
+  const EdgeOffsets eo = edge_offsets(W);
+
+  // Q of the wave's two heads, straight into registers
+  rsrc_t rq[HPW];
+#pragma unroll
+  for (int h = 0; h < HPW; ++h)
+    rq[h] = make_rsrc(reinterpret_cast<const char*>(a.q) + 2 * slice_off(a.sq, b, hw + h, sq.row), span_bytes(L, a.sq[2], D));
+  const uint32_t sq2 = uint32_t(a.sq[2]);
+  u32x4 qn[HPW][KS];
+  auto load_q = [&](int qt) {
+#pragma unroll
+    for (int h = 0; h < HPW; ++h)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        qn[h][ks] = buf_ld16(rq[h], (uint32_t(32 * qt + r32) * sq2 + uint32_t(hf * (D / 2) + 8 * ks)) * 2u);
+  };
+
+  // K/V halves by DMA: the 8 instructions of a half (K positions 64p + lane for p = 0..3, then V)
+  // go two per wave
+  const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * slice_off(a.sk, b, kvh, sq.row), span_bytes(L, a.sk[2], D));
+  const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * slice_off(a.sv, b, kvh, sq.row), span_bytes(L, a.sv[2], D));
+  const int64_t skr = a.sk[2], svr = a.sv[2];
+  uint32_t kv_off[2];
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int ii = 2 * wave + n, p = ii & 3;
+    const int pos = 64 * p + lane, row = pos / CPR, col = (pos % CPR) ^ swz<D>(row);
+    kv_off[n] = uint32_t((int64_t(row) * (ii >= 4 ? svr : skr) + 8 * col) * 2);
+  }
+  const uint32_t hb_k = uint32_t(32 * skr * 2), hb_v = uint32_t(32 * svr * 2);
+  auto load_half = [&](int j, int slot) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int ii = 2 * wave + n;
+      uint16_t* dst = ring + slot * HALF + (ii >= 4 ? TILE : 0) + 512 * (ii & 3);
+      if (ii >= 4) buf_dma16(rv, dst, kv_off[n] + uint32_t(j) * hb_v);
+      else buf_dma16(rk, dst, kv_off[n] + uint32_t(j) * hb_k);
+    }
+  };
+
+  // prologue: the first tile's Q, the sink half and the first tile's window halves
+  load_q(qt0);
+  if (S > 0) load_half(0, NR);
+  for (int j = slide_hlo(qt0, W); j <= qt0; ++j) load_half(j, j % NR);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  for (int qt = qt0; qt < qt1; ++qt) {
+    const int qw = 32 * qt, q = qw + r32;
+    const bool has_next = qt + 1 < qt1;
+    // every wave's share of this tile's halves has landed (each waited for its own loads before
+    // its O stores); in the first tile, the patterns are written
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (has_next) load_half(qt + 1, (qt + 1) % NR);
+    u32x4 qf[HPW][KS];
+#pragma unroll
+    for (int h = 0; h < HPW; ++h)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qf[h][ks] = qn[h][ks] ^ a.qsign;
+    if (has_next) load_q(qt + 1);
+
+    float m2[HPW], lsum[HPW];
+    f32x16 acc[HPW][DB];
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) {
+      m2[h] = kNegInf;
+      lsum[h] = 0.f;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[h][db] = f32x16{};
+    }
+    if (slide_sink_half(qt, W, S))
+      fwd_half<E, D, HPW, 0>(a, ring + NR * HALF, ring + NR * HALF + TILE, 0, qw, q, qf, m2, lsum, acc, pat, eo);
+    for (int j = slide_hlo(qt, W); j <= qt; ++j) {
+      if (!wave_needs(32 * j, qw, L, W, S)) continue;
+      const uint16_t* Kl = ring + (j % NR) * HALF;
+      fwd_half<E, D, HPW, 0>(a, Kl, Kl + TILE, 32 * j, qw, q, qf, m2, lsum, acc, pat, eo);
+    }
+    // the next tile's half and Q have landed (waited before the O stores, which the next tile
+    // does not wait for)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) {
+      float lt = sum_halves(lsum[h]);
+      if (q >= L) continue;
+      float mt = m2[h], r = 1.f;
+      KArgs& A = args_fresh();
+      if (A.sink_logits) {
+        const float sl = A.sink_logits[hw + h] * kLog2e;
+        const float mn = fmaxf(mt, sl);
+        r = fast_exp2(mt - mn);
+        lt = lt * r + fast_exp2(sl - mn);
+        mt = mn;
+      }
+      const float inv = lt > 0.f ? r / lt : 0.f;
+      char* op = reinterpret_cast<char*>(A.o_out) + 2 * slice_off(A.so_out, b, hw + h, sq.row + q);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        float ov[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) ov[e] = acc[h][db][e] * inv;
+        const int d0 = 32 * db + 16 * hf;
+        st16(op + 2 * d0, pack8<E>(ov));
+        st16(op + 2 * (d0 + 8), pack8<E>(ov + 8));
+      }
+      if (hf == 0) A.lse_out[slice_off(A.slse, b, hw + h, sq.row + q)] = (mt + fast_log2(lt)) * kLn2;
+    }
+  }
+}
+
+template <typename E>
+static hipError_t launch_fwd_slide_e(const Args& a, hipStream_t stream) {
+  const dim3 grid(unsigned(a.B * a.Hkv * (a.G / 8) * a.slide_ncu)), block(256);
+  hipLaunchKernelGGL((fwd_slide_kernel<E>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_fwd_slide(const Args& a, int dtype, hipStream_t stream) {
+  return dtype == 1 ? launch_fwd_slide_e<BF16>(a, stream) : launch_fwd_slide_e<F16>(a, stream);
+}
+
 // Resident workgroups per CU of a kernel, remembered per kernel (it depends only on the
 // kernel's resources).
 template <auto Kernel>

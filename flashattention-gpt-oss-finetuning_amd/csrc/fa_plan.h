@@ -75,6 +75,10 @@ FA_HD bool tile_full(int ks0, int qr, int W, int S) {
 // m + 1, loaded during tile m, is not one that tile m reads.
 constexpr int kSlideRing = 7;
 constexpr int kSlideMaxW = 32 * (kSlideRing - 2) + 1;  // 161
+// The sliding forward (fa_fwd.hip fwd_slide_kernel) keeps two workgroups per CU, so its ring is
+// one slot shorter: W <= 129.
+constexpr int kFwdSlideRing = 6;
+constexpr int kFwdSlideMaxW = 32 * (kFwdSlideRing - 2) + 1;  // 129
 
 // First window half of tile m: the half holding key 32m - W + 1 (clamped to 0); W >= 1.
 FA_HD int slide_hlo(int m, int W) {

@@ -61,7 +61,8 @@ static int check_qmajor(int L, int W, int S, int wq) {
   return 0;
 }
 
-// The sliding dQ kernel (1 <= W <= kSlideMaxW, S <= 32): 32-row tiles, each visiting the sink half
+// The sliding dQ kernel and forward (1 <= W <= kSlideMaxW, resp. kFwdSlideMaxW; S <= 32): 32-row
+// tiles, each visiting the sink half
 // (when slide_sink_half) and then the window halves slide_hlo .. m that wave_needs.  Also checks
 // that a tile's halves span at most kSlideRing - 1 indices (the ring slot of half m + 1 is free
 // during tile m) and that, in dq_sink_mode, every tile with rows past dq_sink_row0 visits the sink
@@ -71,6 +72,8 @@ static int check_slide(int L, int W, int S) {
   for (int m = 0; 32 * m < L; ++m) {
     const int qw = 32 * m, hlo = slide_hlo(m, W);
     if (m - hlo > kSlideRing - 2) return fail("slide window spans too many halves", L, W, S, m, qw, hlo, 0);
+    if (W <= kFwdSlideMaxW && m - hlo > kFwdSlideRing - 2)
+      return fail("forward slide window spans too many halves", L, W, S, m, qw, hlo, 0);
     if (dq_sink_mode(L, W, S) && qw + 31 >= dq_sink_row0(L, W) && !slide_sink_half(m, W, S))
       return fail("slide sink rows without the sink half", L, W, S, m, qw, 0, 0);
     auto visit = [&](int ks0) {
