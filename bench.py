@@ -95,8 +95,9 @@ def kernel_accounting(cfg):
     }
 
 
-# Kernels launched by each stage of the C ABI (fa_bwd_dkdv also launches the sink fold).
-STAGE_KERNELS = {"fwd": ["fwd_kernel"], "bwd_dq": ["bwd_dq_kernel"],
+# Kernels launched by each stage of the C ABI: the forward and dQ stages run one of two kernels
+# (the sliding ones for the GPT-OSS sliding layers); fa_bwd_dkdv may also launch the sink fold.
+STAGE_KERNELS = {"fwd": ["fwd_kernel", "fwd_slide_kernel"], "bwd_dq": ["bwd_dq_kernel", "bwd_dq_slide_kernel"],
                  "bwd_dkdv": ["bwd_dkdv_kernel", "bwd_sink_fold_kernel"]}
 
 
@@ -120,7 +121,7 @@ def measured_traffic(config, stage):
         if len(parts) == 4 and parts[0].endswith("_kernel") and parts[3].isdigit():
             rows[parts[0]] = int(parts[3])
     names = STAGE_KERNELS[stage]
-    if names[0] not in rows:
+    if not any(n in rows and not n.startswith("bwd_sink") for n in names):
         return None, None
     src = f"{rel} (committed rocprofv3 --pmc summary, sha256 {hashlib.sha256(data).hexdigest()[:12]})"
     return float(sum(rows.get(n, 0) for n in names)), src
