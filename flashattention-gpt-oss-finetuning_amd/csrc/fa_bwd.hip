@@ -446,6 +446,24 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   }
 }
 
+// dV^T += dO^T P and dK^T += Q^T dS over the DB 32-column blocks of head dim, for one 32-row item:
+// P and dS as B operands (pb, sb: rows 0-15 and 16-31), dO^T / Q^T read transposed from the
+// swizzled row-major tiles Qt and Dt.
+template <typename E, int D, int DB>
+__device__ __forceinline__ void dkdv_products(const uint16_t* Qt, const uint16_t* Dt, const u32x4 (&pb)[2],
+                                              const u32x4 (&sb)[2], f32x16 (&dv)[DB], f32x16 (&dk)[DB]) {
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const u32x4 dt = tr_frag_swz<D>(Dt, 16 * t, 32 * db, D);
+      const u32x4 qt = tr_frag_swz<D>(Qt, 16 * t, 32 * db, D);
+      dv[db] = E::mfma(dt, pb[t], dv[db]);
+      dk[db] = E::mfma(qt, sb[t], dk[db]);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // dK / dV (key-major).  A workgroup owns 64 keys of one KV head; wave (kh, hh) = (wave & 1,
 // wave >> 1) owns the 32-key half kh and takes head slot hh of every step.  A step stages two
@@ -662,7 +680,6 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   auto finish = [&](int buf, int cp, const f32x16& sacc, const f32x16& dpacc) {
     const int qr0 = 32 * (qb_lo + 2 * cp + hh);
     const uint16_t* Qt = lds + buf * STAGE + hh * SLOT;
-    const uint16_t* Dt = Qt + TILE;
     const float* lse2 = reinterpret_cast<const float*>(Qt + 2 * TILE);
     const bool full = !is_chunk && qr0 >= wqlo && qr0 + 32 <= wqhi && tile_full(ks0, qr0, W, S);
     const int m0 = qr0 + 4 * hf - mref;  // mask coordinate of register e = 0
@@ -684,18 +701,9 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
     };
     if (full) elementwise(std::false_type{});
     else elementwise(std::true_type{});
-    const u32x4 pb0 = pack8<E>(p), pb1 = pack8<E>(p + 8);
-    const u32x4 sb0 = pack8<E>(ds), sb1 = pack8<E>(ds + 8);
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const u32x4 dt = tr_frag_swz<D>(Dt, 16 * t, 32 * db, D);
-        const u32x4 qt = tr_frag_swz<D>(Qt, 16 * t, 32 * db, D);
-        dv[db] = E::mfma(dt, t ? pb1 : pb0, dv[db]);
-        dk[db] = E::mfma(qt, t ? sb1 : sb0, dk[db]);
-      }
-    }
+    const u32x4 pb[2] = {pack8<E>(p), pack8<E>(p + 8)};
+    const u32x4 sb[2] = {pack8<E>(ds), pack8<E>(ds + 8)};
+    dkdv_products<E, D, DB>(Qt, Qt + TILE, pb, sb, dv, dk);
   };
 
   // Descriptors are built before any load, whatever the number of steps (a workgroup can own
@@ -794,6 +802,253 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   // sink keys (see fold_sink_keys); the barrier makes its own slot writes visible to all its
   // threads, and every thread is past its last read of the LDS that the fold reuses.
   if (partial_block && !is_chunk && dkdv_folds_in_kernel(a, D)) {
+    __syncthreads();
+    fold_sink_keys<E, D>(b, kvh, min(min(S, kKvKeys), L), sq, reinterpret_cast<float*>(lds));
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// dK / dV with 32-key workgroups (bwd_dkdv4_kernel), for window shapes without chunked sink rows
+// and KV groups of a multiple of 4 query heads (launch_bwd_dkdv picks it; dkdv4_eligible).  A
+// workgroup owns the 32 keys [ks0, ks0 + 32) of one KV head; its 4 waves all hold those keys'
+// K^T / V^T fragments and dK/dV accumulators, and each takes one query head of every group of 4:
+// step (g, qb) is head 4g + wave, 32-row block qb.  Every wave therefore needs the same row blocks,
+// so no wave idles on a block only the other key half sees (bwd_dkdv_kernel's 2-tile steps leave
+// a quarter of its wave-steps idle at W = 128), and the rows of a 32-key half are fewer than those
+// of a 64-key block.  Each wave stages its own items -- its Q and dO tiles and row statistics -- by
+// DMA into its own slot of a 2-stage LDS ring, one step ahead, and waits only for its own loads:
+// the step loop has no barrier.  At the end the four waves' sums are added in LDS in wave order.
+// The per-item mathematics is bwd_dkdv_kernel's.
+// ---------------------------------------------------------------------------------------------
+template <int D>
+__host__ __device__ constexpr int dkdv4_lds_elems() {
+  const int stages = 2 * 4 * (2 * 32 * D + 128);
+  const int red = 3 * 2 * (D >= 32 ? D / 32 : 1) * 16 * 64 * 2;  // fp32 partials of waves 1..3
+  return stages > red ? stages : red;
+}
+
+// Does key block 0's workgroup of bwd_dkdv4_kernel fold the sink keys itself (as
+// dkdv_folds_in_kernel for bwd_dkdv_kernel, with this kernel's LDS)?
+__host__ __device__ inline bool dkdv4_folds_in_kernel(const Args& a, int D, int lds_elems) {
+  return a.sink_dq && (a.S < kKvKeys ? a.S : kKvKeys) * D <= 256 &&
+         ((a.dq_wgs + 3) & ~3) + 4 * 256 <= lds_elems / 2;
+}
+
+template <typename E, int D>
+__global__ __launch_bounds__(256, D == 16 ? 3 : 2) void bwd_dkdv4_kernel(const Args a) {
+  constexpr int KS = D / 16;
+  constexpr int DB = D >= 32 ? D / 32 : 1;
+  constexpr int TILE = 32 * D;
+  constexpr int SLOT = 2 * TILE + 128;  // Q, dO, then lse2[32] and -delta[32] as fp32
+  constexpr int STAGE = 4 * SLOT;       // one slot per wave
+  constexpr int CPR = D / 8;
+  constexpr int IPT = 32 * D * 2 / 1024;  // DMA instructions per tile (1 KiB each)
+  constexpr int PER = 2 * IPT + 1;        // loads per wave and step
+  static_assert(PER <= 63, "vmcnt immediate");
+  constexpr int LDS_ELEMS = dkdv4_lds_elems<D>();
+  __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r32 = lane & 31, hf = lane >> 5;
+  const int W = a.W, S = a.S, G = a.G;
+
+  // workgroups grouped per (b, KV head), n_kblocks 32-key blocks each, groups in (KV head, batch)
+  // order with the KV head outermost (as bwd_dkdv_kernel)
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int grp = id / a.n_kblocks, kblk = id % a.n_kblocks;
+  const int kvh = grp / a.B, b = grp % a.B;
+  const Seq sq = seq_of(a, b);
+  const int L = sq.L;
+  const int ks0 = 32 * kblk;
+  if (ks0 >= L) return;
+  const bool partial_block = a.sink_dq && kblk == 0;  // its sink keys' rows continue in the dQ kernel
+  const int key = ks0 + r32;
+  const int qlo = ks0, qhi = kv4_rows_end(ks0, L, W, S, a.sink_dq != 0);
+
+  u32x4 kf[KS], vf[KS];
+  {
+    const char* kp = reinterpret_cast<const char*>(a.k) + 2 * slice_off(a.sk, b, kvh, sq.row + key);
+    const char* vp = reinterpret_cast<const char*>(a.v) + 2 * slice_off(a.sv, b, kvh, sq.row + key);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d = hf * (D / 2) + 8 * ks;
+      kf[ks] = key < L ? (ld16(kp + 2 * d) ^ a.qsign) : zero16();
+      vf[ks] = key < L ? ld16(vp + 2 * d) : zero16();
+    }
+  }
+  f32x16 dk[DB], dv[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    dk[db] = f32x16{};
+    dv[db] = f32x16{};
+  }
+
+  // steps: (head group g, row block qb), g outermost so that descriptors change once per group
+  const int qb_lo = qlo / 32;
+  const int n_qb = qhi > qlo ? (qhi + 31) / 32 - qb_lo : 0;
+  const int n_steps = (G / 4) * n_qb;
+
+  // staging: this wave's Q and dO tiles (IPT instructions each, lane l of instruction p loading the
+  // global chunk that the swizzle places at 16-byte position 64p + l) and its row statistics
+  // (instruction p covers rows 64p / CPR + lane / CPR: the same swizzle for every p, as the swizzle
+  // depends on the row mod 8 only and 64 / CPR is a multiple of 8)
+  static_assert((64 / CPR) % 8 == 0, "row step of one DMA instruction");
+  const int row0 = lane / CPR, col0 = (lane % CPR) ^ swz<D>(row0);
+  const uint32_t q_off0 = uint32_t((int64_t(row0) * a.sq[2] + 8 * col0) * 2);
+  const uint32_t d_off0 = uint32_t((int64_t(row0) * a.sdo[2] + 8 * col0) * 2);
+  const uint32_t q_step = uint32_t((64 / CPR) * a.sq[2] * 2), d_step = uint32_t((64 / CPR) * a.sdo[2] * 2);
+  const uint32_t bq = uint32_t(64 * a.sq[2]), bd = uint32_t(64 * a.sdo[2]);  // bytes per 32-row block
+  const int nblk = a.Lp / 32;
+  const uint32_t q_bytes = span_bytes(L, a.sq[2], D), d_bytes = span_bytes(L, a.sdo[2], D);
+  int fg = -1;  // head group of the current descriptors
+  rsrc_t rq, rd, rs;
+  auto issue = [&](int s, int buf) {
+    const int g = s / n_qb, qb = qb_lo + s % n_qb;
+    if (g != fg) {
+      fg = g;
+      const int h = kvh * G + 4 * g + wave;
+      rq = make_rsrc(reinterpret_cast<const char*>(a.q) + 2 * slice_off(a.sq, b, h, sq.row), q_bytes);
+      rd = make_rsrc(reinterpret_cast<const char*>(a.dout) + 2 * slice_off(a.sdo, b, h, sq.row), d_bytes);
+      rs = make_rsrc(reinterpret_cast<const char*>(a.delta + (int64_t(b) * a.Hq + h) * nblk * 64), uint32_t(nblk * 256));
+    }
+    uint16_t* dst = lds + buf * STAGE + wave * SLOT;
+#pragma unroll
+    for (int p = 0; p < IPT; ++p) {
+      buf_dma16(rq, dst + 512 * p, q_off0 + uint32_t(p) * q_step + uint32_t(qb) * bq);
+      buf_dma16(rd, dst + TILE + 512 * p, d_off0 + uint32_t(p) * d_step + uint32_t(qb) * bd);
+    }
+    buf_dma4(rs, dst + 2 * TILE, uint32_t(qb) * 256u + 4u * lane);
+  };
+
+  unsigned lim;
+  lim = key < S ? (partial_block ? unsigned(max(qhi - key, 0)) : 0x80000000u) : unsigned(W);
+  // The item of step s: S = Q K^T and dP - delta (accumulated from -delta), then P and dS
+  // elementwise and dV^T += dO^T P, dK^T += Q^T dS (bwd_dkdv_kernel's scores / finish).
+  auto item = [&](int buf, int qb) {
+    const uint16_t* Qt = lds + buf * STAGE + wave * SLOT;
+    const uint16_t* Dt = Qt + TILE;
+    const float* lse2 = reinterpret_cast<const float*>(Qt + 2 * TILE);
+    const float* ndlt = lse2 + 32;
+    const int qr0 = 32 * qb;
+    f32x16 sacc = f32x16{}, dpacc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(ndlt + 8 * j + 4 * hf);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dpacc[4 * j + i] = d4[i];
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int a_off = swz_off<D>(r32, hf * (D / 2) + 8 * ks);
+      sacc = E::mfma(lds16(Qt + a_off), kf[ks], sacc);
+      dpacc = E::mfma(lds16(Dt + a_off), vf[ks], dpacc);
+    }
+    const bool full = qr0 + 32 <= qhi && tile_full(ks0, qr0, W, S);
+    const int m0 = qr0 + 4 * hf - key;
+    float p[16], ds[16];
+    auto elementwise = [&](auto mask_tag) {
+      constexpr bool MASK = decltype(mask_tag)::value;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2 + 8 * j + 4 * hf);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = 4 * j + i;
+          float pe = fast_exp2(fmaf(sacc[e], a.c, -l4[i]));
+          if constexpr (MASK) pe = unsigned(m0 + 8 * j + i) < lim ? pe : 0.f;
+          p[e] = pe;
+          ds[e] = pe * dpacc[e];
+        }
+      }
+    };
+    if (full) elementwise(std::false_type{});
+    else elementwise(std::true_type{});
+    const u32x4 pb[2] = {pack8<E>(p), pack8<E>(p + 8)};
+    const u32x4 sb[2] = {pack8<E>(ds), pack8<E>(ds + 8)};
+    dkdv_products<E, D, DB>(Qt, Qt + TILE, pb, sb, dv, dk);
+  };
+
+  if (n_steps > 0) {
+    issue(0, 0);
+    for (int s = 0; s < n_steps; ++s) {
+      // the next step's items into the other stage (its last reader is this wave's previous
+      // step), then wait for this step's
+      if (s + 1 < n_steps) {
+        issue(s + 1, (s + 1) & 1);
+        wait_vm_lgkm0<PER>();
+      } else {
+        wait_vm_lgkm0<0>();
+      }
+      const int qb = qb_lo + s % n_qb;
+      if (kv_half_needs(32 * qb, ks0, L, W, S)) item(s & 1, qb);  // (the same on every wave)
+    }
+  }
+
+  // ---- add the four waves' sums (wave 0 gets waves 1..3's), fixed order ------------------------
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(lds);
+  if (wave > 0) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        red[(((wave - 1) * 2 + 0) * DB * 16 + db * 16 + e) * 64 + lane] = dk[db][e];
+        red[(((wave - 1) * 2 + 1) * DB * 16 + db * 16 + e) * 64 + lane] = dv[db][e];
+      }
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll 1  // (one wave's sums at a time: unrolled, all 3 * 32 * DB loads are live at once)
+    for (int w = 0; w < 3; ++w)
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          dk[db][e] += red[((w * 2 + 0) * DB * 16 + db * 16 + e) * 64 + lane];
+          dv[db][e] += red[((w * 2 + 1) * DB * 16 + db * 16 + e) * 64 + lane];
+        }
+  }
+
+  // ---- outputs: lane (key, hf) holds head-dim indices 32db + 16hf + e (D == 16: hf == 0) ------
+  if (wave == 0 && key < L) {
+    const bool sink_row = partial_block && key < S;
+    // key block 0's slot of the sink partials (the layout of bwd_dkdv_kernel's)
+    const int64_t blk = int64_t(b * a.Hkv + kvh) * a.nsp;
+    float* pk = partial_block ? a.partial + (blk * (a.n_chunks + 1) + a.n_chunks) * 2 * a.srows * D : nullptr;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      if (D == 16 && hf == 1) continue;
+      const int d0 = 32 * db + (D >= 32 ? 16 * hf : 0);
+      if (sink_row) {
+        float* rk = pk + r32 * D + d0;  // key < srows
+        float* rv = rk + a.srows * D;
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          *reinterpret_cast<f32x4*>(rk + 4 * e4) =
+              f32x4{dk[db][4 * e4], dk[db][4 * e4 + 1], dk[db][4 * e4 + 2], dk[db][4 * e4 + 3]};
+          *reinterpret_cast<f32x4*>(rv + 4 * e4) =
+              f32x4{dv[db][4 * e4], dv[db][4 * e4 + 1], dv[db][4 * e4 + 2], dv[db][4 * e4 + 3]};
+        }
+      } else {
+        char* dkp = reinterpret_cast<char*>(a.dk) + 2 * slice_off(a.sdk, b, kvh, sq.row + key);
+        char* dvp = reinterpret_cast<char*>(a.dv) + 2 * slice_off(a.sdv, b, kvh, sq.row + key);
+        float kv[16], vv[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          kv[e] = dk[db][e] * a.scale;
+          vv[e] = dv[db][e];
+        }
+        st16(dkp + 2 * d0, pack8<E>(kv));
+        st16(dkp + 2 * (d0 + 8), pack8<E>(kv + 8));
+        st16(dvp + 2 * d0, pack8<E>(vv));
+        st16(dvp + 2 * (d0 + 8), pack8<E>(vv + 8));
+      }
+    }
+  }
+  if (partial_block && dkdv4_folds_in_kernel(a, D, LDS_ELEMS)) {
     __syncthreads();
     fold_sink_keys<E, D>(b, kvh, min(min(S, kKvKeys), L), sq, reinterpret_cast<float*>(lds));
   }
@@ -1134,18 +1389,47 @@ static hipError_t launch_dq_d(const Args& a, int, hipStream_t stream) {
   return a.sink_dq ? launch_dq_s<E, D, true>(a, stream) : launch_dq_s<E, D, false>(a, stream);
 }
 
+// bwd_dkdv4_kernel serves 16-bit D <= 64 with KV groups of a multiple of 4 query heads, windows of
+// 1..512 keys and no chunked sink rows (no sink keys past their block's window, or dq_sink_mode),
+// when bwd_dkdv_kernel's grid of 64-key blocks would not give every CU a workgroup (an 8-head
+// shard of a GPT-OSS layer: 64 blocks of 4096 keys).  There its twice as many workgroups, each with
+// fewer rows and no idle waves, finish sooner (measured on MI355X: 19.5 us against 29.5 us at
+// L = 4096, W = 128, 8 heads).  On a full chip of 64-key workgroups bwd_dkdv_kernel is faster (its
+// two key halves share each staged tile), as for full causal and long windows.
+static bool dkdv4_eligible(const Args& a, int D) {
+  return D <= 64 && a.G % 4 == 0 && a.W >= 1 && a.W <= 512 && (a.nsp == 0 || (a.sink_dq && a.n_chunks == 0)) &&
+         int64_t(a.B) * a.Hkv * ((a.L + kKvKeys - 1) / kKvKeys) <= device_cus();
+}
+
 template <typename E, int D>
 static hipError_t launch_dkdv_d(const Args& a, hipStream_t stream) {
-  const dim3 grid(a.n_chunk_wgs + a.B * a.Hkv * a.n_kblocks), block(256);
   Args ad = a;
   // the in-kernel fold finds the dQ slots by the dQ grid (and sizes its run list in LDS by it)
   if (a.sink_dq) ad.dq_wgs = a.dq_slide ? (a.G / 8) * a.slide_ncu : dq_grid<E, D, true>(a);
-  hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), grid, block, 0, stream, ad);
-  hipError_t e = hipGetLastError();
-  // the sink keys are folded inside the dK/dV kernel (dkdv_folds_in_kernel) or by a launch of their own
-  if (e != hipSuccess || a.nsp == 0 || dkdv_folds_in_kernel(ad, D)) return e;
+  hipError_t e;
+  bool folded;
+  if constexpr (D <= 64) {
+    if (dkdv4_eligible(a, D)) {
+      ad.n_kblocks = (a.L + 31) / 32;  // 32-key blocks
+      hipLaunchKernelGGL((bwd_dkdv4_kernel<E, D>), dim3(a.B * a.Hkv * ad.n_kblocks), dim3(256), 0, stream, ad);
+      e = hipGetLastError();
+      folded = dkdv4_folds_in_kernel(ad, D, dkdv4_lds_elems<D>());
+    } else {
+      hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), dim3(a.n_chunk_wgs + a.B * a.Hkv * a.n_kblocks), dim3(256), 0,
+                         stream, ad);
+      e = hipGetLastError();
+      folded = dkdv_folds_in_kernel(ad, D);
+    }
+  } else {
+    hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), dim3(a.n_chunk_wgs + a.B * a.Hkv * a.n_kblocks), dim3(256), 0, stream,
+                       ad);
+    e = hipGetLastError();
+    folded = dkdv_folds_in_kernel(ad, D);
+  }
+  // the sink keys are folded inside the dK/dV kernel or by a launch of their own
+  if (e != hipSuccess || a.nsp == 0 || folded) return e;
   const int64_t n = int64_t(a.B) * a.Hkv * min(a.S, kKvKeys * a.nsp);  // one workgroup per sink key
-  hipLaunchKernelGGL((bwd_sink_fold_kernel<E, D>), dim3(unsigned(n)), block, 0, stream, ad);
+  hipLaunchKernelGGL((bwd_sink_fold_kernel<E, D>), dim3(unsigned(n)), dim3(256), 0, stream, ad);
   return hipGetLastError();
 }
 

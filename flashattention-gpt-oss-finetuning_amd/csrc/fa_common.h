@@ -210,6 +210,13 @@ __device__ __forceinline__ void wait_vm_lgkm0_barrier() {
   asm volatile("s_waitcnt %0\n\ts_barrier" ::"n"(waitcnt_vm_lgkm0(VM)) : "memory");
 }
 
+// The same wait without the barrier: for LDS that only the waiting wave's own DMA writes.
+template <int VM>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(VM >= 0 && VM <= 63, "vmcnt range");
+  asm volatile("s_waitcnt %0" ::"n"(waitcnt_vm_lgkm0(VM)) : "memory");
+}
+
 // Bytes spanned by `rows` fp32 values with stride `stride` (0 if none).
 __device__ __forceinline__ uint32_t span_f32(int rows, int64_t stride) {
   return rows > 0 ? uint32_t((int64_t(rows - 1) * stride + 1) * 4) : 0u;

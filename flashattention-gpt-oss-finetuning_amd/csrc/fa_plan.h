@@ -147,4 +147,15 @@ FA_HD bool dq_sink_mode(int L, int W, int S) { return S >= 1 && S <= kDqSinkKeys
 
 FA_HD int dq_sink_row0(int L, int W) { return kv_window_end(0, L, W); }
 
+// ---- key-major kernel with 32-key workgroups (bwd_dkdv4_kernel) ---------------------------------
+// A workgroup owns the 32 keys [ks0, ks0 + 32) and its 4 waves take 4 query heads at a time, each
+// staging its own (head, 32-row block) items, so every wave needs the same row blocks.  It sweeps
+// rows [ks0, kv4_rows_end): the window's rows, and for a half holding sink keys every later row
+// (up to dq_sink_row0 in dq_sink_mode, where the dQ kernel takes the rest).  It serves only shapes
+// without chunked sink rows (nsp == 0, or dq_sink_mode).
+FA_HD int kv4_rows_end(int ks0, int L, int W, int S, bool dq_sink) {
+  if (ks0 < S) return dq_sink ? dq_sink_row0(L, W) : L;
+  return kv_rows_end(ks0, 32, L, W);
+}
+
 }  // namespace fa

@@ -1,8 +1,8 @@
 // plan_check.cpp - host check of the kernels' visit plan (csrc/fa_plan.h compiled with g++).
 //
 // Walks the loops of the query-major kernels (fa_fwd.hip fwd_kernel, fa_bwd.hip bwd_dq_kernel,
-// fa_bwd_slide.hip bwd_dq_slide_kernel) and of the key-major kernel (bwd_dkdv_kernel) over many (L, W, S, rows-per-workgroup,
-// chunk size) cases and checks that
+// fa_bwd_slide.hip bwd_dq_slide_kernel) and of the key-major kernels (bwd_dkdv_kernel,
+// bwd_dkdv4_kernel) over many (L, W, S, rows-per-workgroup, chunk size) cases and checks that
 //   * every allowed (q, k) pair is visited exactly once and no other pair is counted,
 //   * a tile reported "full" (mask skipped) holds only allowed pairs,
 //   * the key-major row ranges of the regular and chunk workgroups partition the rows that can
@@ -101,6 +101,29 @@ static int check_slide(int L, int W, int S) {
   return 0;
 }
 
+// In dq_sink_mode, the dQ kernel's sink rows: every query tile of wq 32-row waves visits keys
+// [0, 32) through its plan; rows >= dq_sink_row0 add keys [0, kDqSinkKeys) where allowed, keys < S
+// counted.
+static int count_dq_sink_rows(std::vector<int>& cnt, int L, int W, int S) {
+  if (S > kDqSinkKeys) return fail("dq sink mode with too many sink keys", L, W, S, 0, 0, 0, S);
+  const int row0 = dq_sink_row0(L, W);
+  for (int wq : {1, 2, 4})
+    for (int q0 = 0; q0 < L; q0 += 32 * wq) {
+      const QPlan p = qplan(q0, 32 * wq, L, W, S);
+      const bool visits0 = p.nb > 0 && qplan_block(p, 0) == 0;
+      for (int w = 0; w < wq; ++w) {
+        const int qw = q0 + 32 * w;
+        if (qw >= L || qw + 31 < row0) continue;
+        if (!visits0 || !wave_needs(0, qw, L, W, S)) return fail("dq sink tile misses key block 0", L, W, S, wq, qw, 0, 0);
+        if (wq != 1) continue;  // count once
+        for (int q = qw; q < qw + 32 && q < L; ++q)
+          for (int k = 0; k < S; ++k)
+            if (q >= row0 && allowed(q - k, k, W, S)) ++cnt[size_t(q) * L + k];
+      }
+    }
+  return 0;
+}
+
 // Key-major: regular workgroups per kKvKeys-key block (waves per 32-key half), plus chunk
 // workgroups for the sink blocks.  A wave sweeps the workgroup's rows from its own first key on,
 // skipping q-blocks that kv_half_needs rules out, and, in a chunk workgroup, halves without sink
@@ -142,24 +165,8 @@ static int check_kvmajor(int L, int W, int S, int chunk_rows) {
   for (int kblk = 0; kblk < nkb; ++kblk)
     if (sweep(kblk, kKvKeys * kblk, kv_window_end(kblk, L, W), false)) return 1;
   if (dq_sink_mode(L, W, S)) {
-    // the dQ kernel's sink rows: every query tile of wq 32-row waves visits keys [0, 32) through
-    // its plan; rows >= dq_sink_row0 add keys [0, kDqSinkKeys) where allowed, keys < S counted
-    if (S > kDqSinkKeys || nsp != 1) return fail("dq sink mode with too many sink keys", L, W, S, chunk_rows, 0, 0, nsp);
-    const int row0 = dq_sink_row0(L, W);
-    for (int wq : {1, 2, 4})
-      for (int q0 = 0; q0 < L; q0 += 32 * wq) {
-        const QPlan p = qplan(q0, 32 * wq, L, W, S);
-        const bool visits0 = p.nb > 0 && qplan_block(p, 0) == 0;
-        for (int w = 0; w < wq; ++w) {
-          const int qw = q0 + 32 * w;
-          if (qw >= L || qw + 31 < row0) continue;
-          if (!visits0 || !wave_needs(0, qw, L, W, S)) return fail("dq sink tile misses key block 0", L, W, S, wq, qw, 0, 0);
-          if (wq != 1) continue;  // count once
-          for (int q = qw; q < qw + 32 && q < L; ++q)
-            for (int k = 0; k < S; ++k)
-              if (q >= row0 && allowed(q - k, k, W, S)) ++cnt[size_t(q) * L + k];
-        }
-      }
+    if (nsp != 1) return fail("dq sink mode with too many sink keys", L, W, S, chunk_rows, 0, 0, nsp);
+    if (count_dq_sink_rows(cnt, L, W, S)) return 1;
   } else {
     for (int kblk = 0; kblk < nsp; ++kblk)
       for (int c = 0; c < n_chunks; ++c)
@@ -169,6 +176,45 @@ static int check_kvmajor(int L, int W, int S, int chunk_rows) {
     for (int k = 0; k < L; ++k) {
       const int want = ref_allowed(q, k, W, S) ? 1 : 0;
       if (cnt[size_t(q) * L + k] != want) return fail("kv-major visit count", L, W, S, chunk_rows, q, k, cnt[size_t(q) * L + k]);
+    }
+  return 0;
+}
+
+// Key-major with 32-key workgroups (fa_bwd.hip bwd_dkdv4_kernel; shapes with nsp == 0 or in
+// dq_sink_mode): keys [ks0, ks0 + 32) sweep the 32-row blocks of [ks0, kv4_rows_end) that
+// kv_half_needs keeps, with the kernel's own mask: key k passes row q when 0 <= q - k < lim(k),
+// lim = W for window keys, rows_end - k for sink keys whose later rows the dQ kernel takes, and
+// unbounded for other sink keys.  Pairs with q >= L or k >= L may pass the mask: their Q rows and
+// K rows are zero-filled and their dK/dV rows are never stored, so only pairs inside L are counted.
+static int check_kv4(int L, int W, int S) {
+  const bool dqs = dq_sink_mode(L, W, S);
+  if (!(kv_sink_blocks(L, W, S) == 0 || dqs)) return 0;  // not served by this kernel
+  std::vector<int> cnt(size_t(L) * L, 0);
+  for (int ks0 = 0; ks0 < L; ks0 += 32) {
+    const int qlo = ks0, qhi = kv4_rows_end(ks0, L, W, S, dqs);
+    if (qhi <= qlo) continue;
+    for (int qb = qlo / 32; qb < (qhi + 31) / 32; ++qb) {
+      const int qr0 = 32 * qb;
+      if (!kv_half_needs(qr0, ks0, L, W, S)) continue;
+      const bool full = qr0 + 32 <= qhi && tile_full(ks0, qr0, W, S);
+      for (int r = 0; r < 32; ++r)
+        for (int c = 0; c < 32; ++c) {
+          const int q = qr0 + r, k = ks0 + c;
+          const long lim = k < S ? (dqs ? long(imax(qhi - k, 0)) : 0x80000000L) : long(W);
+          const bool ok = full || (q - k >= 0 && long(q - k) < lim);
+          if (!ok) continue;
+          if (full && (q >= L || k >= L || !ref_allowed(q, k, W, S)))
+            return fail("full kv4 tile has a masked pair", L, W, S, 32, q, k, 0);
+          if (q >= L || k >= L) continue;
+          ++cnt[size_t(q) * L + k];
+        }
+    }
+  }
+  if (dqs && count_dq_sink_rows(cnt, L, W, S)) return 1;
+  for (int q = 0; q < L; ++q)
+    for (int k = 0; k < L; ++k) {
+      const int want = ref_allowed(q, k, W, S) ? 1 : 0;
+      if (cnt[size_t(q) * L + k] != want) return fail("kv4 visit count", L, W, S, 32, q, k, cnt[size_t(q) * L + k]);
     }
   return 0;
 }
@@ -189,6 +235,10 @@ int main() {
         }
         for (int cr : {32, 64, 256}) {
           if (check_kvmajor(L, W, S, cr)) return 1;
+          ++cases;
+        }
+        if (W >= 1 && W <= 512) {
+          if (check_kv4(L, W, S)) return 1;
           ++cases;
         }
         if (W >= 1 && W <= kSlideMaxW && S <= 32) {
