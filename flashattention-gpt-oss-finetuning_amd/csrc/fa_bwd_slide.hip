@@ -232,11 +232,41 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
       }
     };
 
+    // The sink half with S <= 8 (when it is not a window half: every row's window starts at key
+    // 32 or later, and every row is past key 31): only keys [0, 8) can be allowed, which are
+    // registers 0..3 of each lane (keys 4hf + e), so P and dS are computed for those four, the
+    // rest are 0, and dQ^T += K^T dS^T takes keys [0, 16) only.
+    auto sink_half8 = [&](const uint16_t* Kl, float (&p)[16], float (&ds)[16]) {
+      const uint16_t* Vl = Kl + TILE;
+      f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int off = swz_off<D>(r32, hf * (D / 2) + 8 * ks);
+        s = E::mfma(*reinterpret_cast<const u32x4*>(Kl + off), qf[ks], s);
+        dp = E::mfma(*reinterpret_cast<const u32x4*>(Vl + off), dof[ks], dp);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        p[e] = 0.f;
+        ds[e] = 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float pe = fast_exp2(fmaf(s[e], a.c, -lse2));
+        p[e] = 4 * hf + e < S ? pe : 0.f;
+        ds[e] = p[e] * (dp[e] + ndelta);
+      }
+      const u32x4 d0 = pack8<E>(ds);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[db] = E::mfma(tr_frag_swz<D>(Kl, 0, 32 * db, D), d0, acc[db]);
+    };
+
     const int hlo = slide_hlo(qt, W);
     // the sink half, when it is not one of the window halves (its keys >= S are then all masked)
     if (slide_sink_half(qt, W, S)) {
       float p[16], ds[16];
-      half_step(ring + kRing * HALF, 0, p, ds);
+      if (S <= 8) sink_half8(ring + kRing * HALF, p, ds);
+      else half_step(ring + kRing * HALF, 0, p, ds);
       if constexpr (SINK) {
         if (qw + 31 >= sink_row0) {
           // P and dS of keys [0, 16) of rows >= sink_row0 into the [32 rows][16 keys] tiles, then

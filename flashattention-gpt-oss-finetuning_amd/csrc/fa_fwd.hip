@@ -195,6 +195,65 @@ __device__ __forceinline__ void fwd_half(const Args& a, const uint16_t* Kl, cons
   }
 }
 
+// fwd_half for the sliding forward's separate sink half with S <= 8: keys [0, 32), none of them in
+// a row's window and every row past key 31, so only keys [0, 8) can be allowed -- registers 0..3
+// of each lane (keys 4hf + e).  Their P is computed, the rest is 0, and O^T += V^T P^T takes keys
+// [0, 16) only (one product per 32 columns instead of two).
+template <typename E, int D, int HPW>
+__device__ __forceinline__ void fwd_sink_half8(const Args& a, const uint16_t* Kl, const uint16_t* Vl,
+                                               const u32x4 (&qf)[HPW][kQFrags<D, 0>], float (&m2)[HPW],
+                                               float (&lsum)[HPW], f32x16 (&acc)[HPW][D >= 32 ? D / 32 : 1]) {
+  constexpr int DB = D >= 32 ? D / 32 : 1;
+  constexpr int KS = kQFrags<D, 0>;
+  const int lane = threadIdx.x & 63;
+  const int r32 = lane & 31, hf = lane >> 5;
+  u32x4 kf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const u32x4*>(Kl + swz_off<D>(r32, hf * (D / 2) + 8 * ks));
+  f32x16 s[HPW];
+#pragma unroll
+  for (int h = 0; h < HPW; ++h) {
+    s[h] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) s[h] = E::mfma(kf[ks], qf[h][ks], s[h]);
+  }
+  u32x4 vf[DB];  // V^T over keys [0, 16)
+#pragma unroll
+  for (int db = 0; db < DB; ++db) vf[db] = tr_frag_swz<D>(Vl, 0, 32 * db, D);
+  bool ok[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) ok[e] = 4 * hf + e < a.S;
+#pragma unroll
+  for (int h = 0; h < HPW; ++h) {
+    float m = kNegInf;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) m = ok[e] ? fmaxf(m, s[h][e]) : m;
+    const float mx = max_halves(m) * a.c;  // key 0 is allowed on every row: finite
+    if (wave_any(mx > m2[h] + kRescaleGap)) {  // (fwd_half's lazy rescaling)
+      const float mnew = fmaxf(m2[h], mx);
+      const float alpha = mnew == kNegInf ? 1.f : fast_exp2(m2[h] - mnew);
+      m2[h] = mnew;
+      lsum[h] *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[h][db] *= alpha;
+    }
+    const float ms = m2[h] == kNegInf ? 0.f : m2[h];
+    float sv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sv[e] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float pe = fast_exp2(fmaf(s[h][e], a.c, -ms));
+      sv[e] = ok[e] ? pe : 0.f;
+    }
+    const u32x4 pb0 = pack8<E>(sv);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[h][db] = E::mfma(vf[db], pb0, acc[h][db]);
+    lsum[h] = E::sum2(pb0[0], lsum[h]);
+    lsum[h] = E::sum2(pb0[1], lsum[h]);
+  }
+}
+
 // P V on the fp8 matrix cores (F8 = 2): one 64-key block [kb, kb + 64) -- swizzled e4m3 K and V
 // tiles at Kl, Vl, both laid out like 16-bit rows of D / 2 elements -- for the HPW heads of the
 // wave.  v_mfma_scale_f32_32x32x64 reduces over 64 keys, so both halves' scores come first (a half
@@ -728,8 +787,10 @@ __global__ __launch_bounds__(256, 2) void fwd_slide_kernel(const Args a) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) acc[h][db] = f32x16{};
     }
-    if (slide_sink_half(qt, W, S))
-      fwd_half<E, D, HPW, 0>(a, ring + NR * HALF, ring + NR * HALF + TILE, 0, qw, q, qf, m2, lsum, acc, pat, eo);
+    if (slide_sink_half(qt, W, S)) {
+      if (S <= 8) fwd_sink_half8<E, D, HPW>(a, ring + NR * HALF, ring + NR * HALF + TILE, qf, m2, lsum, acc);
+      else fwd_half<E, D, HPW, 0>(a, ring + NR * HALF, ring + NR * HALF + TILE, 0, qw, q, qf, m2, lsum, acc, pat, eo);
+    }
     for (int j = slide_hlo(qt, W); j <= qt; ++j) {
       if (!wave_needs(32 * j, qw, L, W, S)) continue;
       const uint16_t* Kl = ring + (j % NR) * HALF;
