@@ -446,6 +446,37 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   }
 }
 
+// K^T / V^T operands of a dK/dV wave (B of S = Q K^T and dP = dO V^T): lane (key, hf), head-dim
+// slice [hf D/2 + 8ks, +8), through buffer resources over the KV head's rows [0, L), so keys >= L
+// read as zero with no per-lane select -- nothing uses the registers, and so nothing waits for
+// them, until kv_operands_ready.  (K keeps its sign: the kernels take a negative softmax scale
+// in the exponent's factor.)
+template <int D>
+__device__ __forceinline__ void load_kv_operands(const Args& a, int b, int kvh, const Seq& sq, int key,
+                                                 u32x4 (&kf)[D / 16], u32x4 (&vf)[D / 16]) {
+  const int hf = (threadIdx.x >> 5) & 1;
+  const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * slice_off(a.sk, b, kvh, sq.row),
+                              span_bytes(sq.L, a.sk[2], D));
+  const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * slice_off(a.sv, b, kvh, sq.row),
+                              span_bytes(sq.L, a.sv[2], D));
+  const uint32_t ko = uint32_t(int64_t(key) * a.sk[2] * 2), vo = uint32_t(int64_t(key) * a.sv[2] * 2);
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) {
+    const uint32_t d2 = uint32_t(2 * (hf * (D / 2) + 8 * ks));
+    kf[ks] = buf_ld16(rk, ko + d2);
+    vf[ks] = buf_ld16(rv, vo + d2);
+  }
+}
+// Where the K/V operand loads must have landed: an empty asm statement that reads and rewrites
+// the registers, so the compiler's own wait for them goes here -- after the caller's first DMA
+// issues, which stay in flight -- and not before the first product inside the step loop, where it
+// would be repeated every step and wait for the DMA of later steps too.
+template <int KS>
+__device__ __forceinline__ void kv_operands_ready(u32x4 (&kf)[KS], u32x4 (&vf)[KS]) {
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kf[ks]), "+v"(vf[ks]));
+}
+
 // dV^T += dO^T P and dK^T += Q^T dS over the DB 32-column blocks of head dim, for one 32-row item:
 // P and dS as B operands (pb, sb: rows 0-15 and 16-31), dO^T / Q^T read transposed from the
 // swizzled row-major tiles Qt and Dt.
@@ -550,20 +581,10 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   const bool wave_on = ks0 < L && (!is_chunk || ks0 < S);
   const int wqlo = is_chunk ? qlo : max(qlo, ks0), wqhi = qhi;
 
-  // K^T / V^T operands (B of S = Q K^T and dP = dO V^T): lane (key, hf), head-dim slice
-  // [hf*D/2 + 8ks, +8).  A negative softmax scale flips the sign of K here (exact), so scores
-  // need no per-item sign handling.
+  // K^T / V^T operands, waited for after the first DMA issues (load_kv_operands)
   u32x4 kf[KS], vf[KS];
-  {
-    const char* kp = reinterpret_cast<const char*>(a.k) + 2 * slice_off(a.sk, b, kvh, sq.row + key);
-    const char* vp = reinterpret_cast<const char*>(a.v) + 2 * slice_off(a.sv, b, kvh, sq.row + key);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int d = hf * (D / 2) + 8 * ks;
-      kf[ks] = key < L ? (ld16(kp + 2 * d) ^ a.qsign) : zero16();
-      vf[ks] = key < L ? ld16(vp + 2 * d) : zero16();
-    }
-  }
+  load_kv_operands<D>(a, b, kvh, sq, key, kf, vf);
+  const float cs = a.qsign ? -a.c : a.c;  // exponent factor: scale log2(e), with its sign
 
   f32x16 dk[DB], dv[DB];
 #pragma unroll
@@ -692,7 +713,7 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int e = 4 * j + i;
-          float pe = fast_exp2(fmaf(sacc[e], a.c, -l4[i]));
+          float pe = fast_exp2(fmaf(sacc[e], cs, -l4[i]));
           if constexpr (MASK) pe = unsigned(m0 + 8 * j + i) < lim ? pe : 0.f;
           p[e] = pe;
           ds[e] = pe * dpacc[e];
@@ -716,6 +737,7 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   if (n_steps > 0) {
     // loads NSTG - 1 steps ahead; step s waits for its own
     for (int k = 0; k < NSTG - 1; ++k) issue(k);
+    kv_operands_ready(kf, vf);
     int cp = 0, cur = 0, nxt = NSTG - 1;  // stage of step s, stage of step s + NSTG - 1
     for (int s = 0; s < n_steps; ++s) {
       wait_vm_lgkm0_barrier<(NSTG - 2) * PER>();  // step s landed everywhere
@@ -868,16 +890,8 @@ __global__ __launch_bounds__(256, D == 16 ? 3 : 2) void bwd_dkdv4_kernel(const A
   const int qlo = ks0, qhi = kv4_rows_end(ks0, L, W, S, a.sink_dq != 0);
 
   u32x4 kf[KS], vf[KS];
-  {
-    const char* kp = reinterpret_cast<const char*>(a.k) + 2 * slice_off(a.sk, b, kvh, sq.row + key);
-    const char* vp = reinterpret_cast<const char*>(a.v) + 2 * slice_off(a.sv, b, kvh, sq.row + key);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int d = hf * (D / 2) + 8 * ks;
-      kf[ks] = key < L ? (ld16(kp + 2 * d) ^ a.qsign) : zero16();
-      vf[ks] = key < L ? ld16(vp + 2 * d) : zero16();
-    }
-  }
+  load_kv_operands<D>(a, b, kvh, sq, key, kf, vf);
+  const float cs = a.qsign ? -a.c : a.c;  // exponent factor: scale log2(e), with its sign
   f32x16 dk[DB], dv[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
@@ -956,7 +970,7 @@ __global__ __launch_bounds__(256, D == 16 ? 3 : 2) void bwd_dkdv4_kernel(const A
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int e = 4 * j + i;
-          float pe = fast_exp2(fmaf(sacc[e], a.c, -l4[i]));
+          float pe = fast_exp2(fmaf(sacc[e], cs, -l4[i]));
           if constexpr (MASK) pe = unsigned(m0 + 8 * j + i) < lim ? pe : 0.f;
           p[e] = pe;
           ds[e] = pe * dpacc[e];
@@ -972,6 +986,7 @@ __global__ __launch_bounds__(256, D == 16 ? 3 : 2) void bwd_dkdv4_kernel(const A
 
   if (n_steps > 0) {
     issue(0, 0);
+    kv_operands_ready(kf, vf);
     for (int s = 0; s < n_steps; ++s) {
       // the next step's items into the other stage (its last reader is this wave's previous
       // step), then wait for this step's
