@@ -82,14 +82,21 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
     const int col = 8 * (((64 * p + lane) % CPR) ^ swz<D>(tr));
     st_off[p] = uint32_t(tr) << 16 | uint32_t(col);
   }
-  auto stash_rows = [&](int qt) {
+  // one of the tile's three row tiles (part 0: Q, 1: dO, 2: O), KS instructions
+  auto stash_part = [&](int qt, int part) {
+    const rsrc_t r = part == 0 ? rq : part == 1 ? rd : ro;
+    const uint32_t rs = part == 0 ? sq2 : part == 1 ? sdo2 : so2;
 #pragma unroll
     for (int p = 0; p < KS; ++p) {
-      const uint32_t row = uint32_t(32 * qt) + (st_off[p] >> 16), col = st_off[p] & 0xffffu;
-      buf_dma16(rq, stash + 0 * TILE + 512 * p, (row * sq2 + col) * 2);
-      buf_dma16(rd, stash + 1 * TILE + 512 * p, (row * sdo2 + col) * 2);
-      buf_dma16(ro, stash + 2 * TILE + 512 * p, (row * so2 + col) * 2);
+      uint32_t so = st_off[p];
+      asm volatile("" : "+v"(so));  // computed here: hoisted, the offsets of every part stay live
+      const uint32_t row = uint32_t(32 * qt) + (so >> 16), col = so & 0xffffu;
+      buf_dma16(r, stash + part * TILE + 512 * p, (row * rs + col) * 2);
     }
+  };
+  auto stash_rows = [&](int qt) {
+#pragma unroll
+    for (int part = 0; part < 3; ++part) stash_part(qt, part);
   };
   auto load_lse = [&](int qt) { return buf_ldf(rl, uint32_t(32 * qt + r32) * uint32_t(a.slse[2]) * 4u); };
 
@@ -167,14 +174,27 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
     f32x16 acc[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
-    // the next tile's rows, once this tile's have been read out of the stash (after the sink half
-    // on the sink path, which also reads the stash)
-    auto refill = [&]() {
+    // The next tile's rows, once this tile's have been read out of the stash (after the sink half
+    // on the sink path, which also reads the stash), in three parts issued between the window
+    // halves: issued at once, a wave's 3 KS DMA instructions stall it while the CU's load path
+    // takes the whole workgroup's 96 KB.  Part 2 also loads the next tile's LSE.
+    int refilled = 0;  // parts issued
+    auto refill_part = [&]() {
       if (has_next) {
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        stash_rows(qt + 1);
-        lse_next = load_lse(qt + 1);
+        switch (refilled) {  // (constant parts: a run-time part index would put the descriptors on the stack)
+          case 0:
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            stash_part(qt + 1, 0);
+            break;
+          case 1: stash_part(qt + 1, 1); break;
+          case 2:
+            stash_part(qt + 1, 2);
+            lse_next = load_lse(qt + 1);
+            break;
+          default: break;
+        }
       }
+      ++refilled;
     };
 
     // One 32-key half from LDS: S^T = K Q^T and dP^T - delta = V dO^T - delta (lane = query row),
@@ -308,7 +328,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
       if (has_next) wait_vm_lgkm0_barrier<1>();
       else wait_vm_lgkm0_barrier<0>();
     }
-    refill();
+    refill_part();
     {
       // the row statistics for the dK/dV kernel (stored here, after the first tile's wait above)
       KArgs& A = args_fresh();
@@ -324,12 +344,14 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
         if (lane == 0) A.dsink_part[(int64_t(b) * A.Hq + h) * (A.Lp / 32) + qt] = -v;
       }
     }
-    // the window halves
+    // the window halves, with the rest of the refill after the first two
     for (int j = hlo; j <= qt; ++j) {
       if (!wave_needs(32 * j, qw, L, W, S)) continue;
       float p[16], ds[16];
       half_step(ring + (j % kRing) * HALF, 32 * j, p, ds);
+      if (refilled < 3) refill_part();
     }
+    while (refilled < 3) refill_part();
     // the next tile's rows and K/V half have landed (waited before this tile's dQ stores, which
     // the next tile does not wait for)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
