@@ -68,7 +68,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   // the P / dS transposition tiles of the sink path: in the wave's O tile (read only for delta at
   // the start of a tile), or, for D = 16 where that tile is too small, in a region of their own
   constexpr int PT_EXTRA = (SINK && D < 32) ? 4 * 1024 : 0;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * BUF + 4 * STASH + PT_EXTRA];
+  // Small head dims (D <= 32): a key block's compute is short next to the latency of fetching the
+  // next one, so (as in the forward) every block of a tile, up to NBUF at a time, is fetched at
+  // once by LDS DMA into a buffer of its own and the blocks are then computed back to back; the
+  // first tile's rows come in the same round trip.  Wider heads double-buffer through registers.
+  constexpr bool PRE = D <= 32;
+  constexpr int NBUF = PRE ? 32768 / (2 * BUF) : 2;  // 32 KiB of K/V blocks
+  __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF * BUF + 4 * STASH + PT_EXTRA];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -120,7 +126,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   // it loads the global chunk that the swizzle places there), where they occupy no registers
   // while the current tile computes; the row's lse goes to a register.  Buffer resources over the
   // sequence's rows [0, L) of the head: rows past L read as zero.
-  uint16_t* stash = lds + 2 * BUF + wave * STASH;
+  uint16_t* stash = lds + NBUF * BUF + wave * STASH;
   constexpr int CPR = D / 8;  // 16-byte chunks per row
   auto stash_rows = [&](const TileIdx& t) {
     KArgs& A = args_fresh();
@@ -166,12 +172,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
       dvs[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
-  uint16_t* ptile = SINK ? (D >= 32 ? stash + 2 * TILE : lds + 2 * BUF + 4 * STASH + wave * 1024) : nullptr;
+  uint16_t* ptile = SINK ? (D >= 32 ? stash + 2 * TILE : lds + NBUF * BUF + 4 * STASH + wave * 1024) : nullptr;
 
   int tile = t_lo + pos;
   int run_first = tile;  // first tile of the current run of tiles of one (batch, KV head)
   float lse_next = 0.f;
-  if (tile < t_hi) {
+  const int first_tile = tile;
+  if (!PRE && tile < t_hi) {
     const TileIdx t0 = decode(tile);
     stash_rows(t0);
     lse_next = load_lse(t0);
@@ -182,6 +189,38 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
     const int qw = t.qw, q = qw + r32, L = t.L;
     const bool wave_active = qw < L;
     const bool has_next = tile + wgs_x < t_hi;
+
+    const QPlan plan = qplan(t.q0, 32 * a.wq, L, W, S);
+    KArgs& Akv = args_fresh();
+    const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(Akv.k) + 2 * slice_off(Akv.sk, t.b, t.kvh, t.row), span_bytes(L, Akv.sk[2], D));
+    const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(Akv.v) + 2 * slice_off(Akv.sv, t.b, t.kvh, t.row), span_bytes(L, Akv.sv[2], D));
+    // PRE: DMA of a 64-key block into buffer j -- the block's K and V tiles are CPB 16-byte chunks
+    // each, 2 CPB / 64 instructions of 64 lanes; wave w issues instructions [w NIW, (w + 1) NIW),
+    // and lane l of instruction p (of K or V) loads the chunk that the swizzle places at position
+    // 64 p + l (as the forward's)
+    constexpr int IPT = CPB / 64;
+    constexpr int NIW = PRE ? 2 * IPT / 4 : 1;
+    static_assert(!PRE || (NIW >= 1 && 2 * IPT == 4 * NIW), "whole DMA instructions per wave");
+    auto dma_block = [&](int kb, int j) {
+#pragma unroll
+      for (int n = 0; n < NIW; ++n) {
+        const int ii = wave * NIW + n, is_v = ii >= IPT, pi = is_v ? ii - IPT : ii;
+        const int dpos = 64 * pi + lane, row = dpos / CPR, col = (dpos % CPR) ^ swz<D>(row);
+        uint16_t* dst = lds + j * BUF + (is_v ? BN * D : 0) + 512 * pi;
+        const uint32_t off = uint32_t(int64_t(kb + row) * (is_v ? bv : bk)) + 16u * uint32_t(col);
+        if (is_v) buf_dma16(rv, dst, off);
+        else buf_dma16(rk, dst, off);
+      }
+    };
+    if constexpr (PRE) {
+      const int ng = min(NBUF, plan.nb);
+      for (int j = 0; j < ng; ++j) dma_block(qplan_block(plan, j), j);
+      if (tile == first_tile) {  // the first tile's rows, in the same round trip as its blocks
+        stash_rows(t);
+        lse_next = load_lse(t);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+    }
 
     // Row operands and row statistics, from the stash (this wave's own DMA, complete by now:
     // see the wait after the key loop).  delta = rowsum(dO o O) is stored for the dK/dV kernel;
@@ -227,10 +266,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
 
-    const QPlan plan = qplan(t.q0, 32 * a.wq, L, W, S);
-    KArgs& Akv = args_fresh();
-    const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(Akv.k) + 2 * slice_off(Akv.sk, t.b, t.kvh, t.row), span_bytes(L, Akv.sk[2], D));
-    const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(Akv.v) + 2 * slice_off(Akv.sv, t.b, t.kvh, t.row), span_bytes(L, Akv.sv[2], D));
     u32x4 kreg[NK], vreg[NK];
     auto gload = [&](int kb) {
 #pragma unroll
@@ -263,19 +298,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
       }
     };
 
-    if (plan.nb > 0) {  // (a tile past its sequence's end, in a variable-length batch, has none)
-      gload(qplan_block(plan, 0));
-      sstore(0);
-      __syncthreads();
-    }
-
-    for (int i = 0; i < plan.nb; ++i) {
-      const int kb = qplan_block(plan, i);
-      const bool more = i + 1 < plan.nb;
-      if (more) gload(qplan_block(plan, i + 1));
-      if (!SINK && i == 0) refill();
+    // one key block [kb, kb + 64) from the K tile at Kl (V follows it)
+    auto compute_block = [&](int kb, const uint16_t* Kl) {
       if (wave_active) {
-        const uint16_t* Kl = lds + (i & 1) * BUF;
         const uint16_t* Vl = Kl + BN * D;
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
@@ -376,9 +401,42 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
           }
         }
       }
-      if (SINK && i == 0) refill();
-      if (more) sstore((i + 1) & 1);
-      __syncthreads();
+    };
+
+    if constexpr (PRE) {
+      for (int g0 = 0; g0 < plan.nb; g0 += NBUF) {
+        const int ng = min(NBUF, plan.nb - g0);
+        if (g0 > 0)
+          for (int j = 0; j < ng; ++j) dma_block(qplan_block(plan, g0 + j), j);
+        // the blocks have landed everywhere (the next tile's rows may be in flight)
+        if (g0 == 0 && !SINK) {
+          refill();
+          if (has_next) wait_vm_lgkm0_barrier<3 * KS + 1>();
+          else wait_vm_lgkm0_barrier<0>();
+        } else {
+          wait_vm_lgkm0_barrier<0>();
+        }
+        for (int j = 0; j < ng; ++j) {
+          compute_block(qplan_block(plan, g0 + j), lds + j * BUF);
+          if (SINK && g0 == 0 && j == 0) refill();
+        }
+        __syncthreads();  // before the buffers are refilled
+      }
+    } else {
+      if (plan.nb > 0) {  // (a tile past its sequence's end, in a variable-length batch, has none)
+        gload(qplan_block(plan, 0));
+        sstore(0);
+        __syncthreads();
+      }
+      for (int i = 0; i < plan.nb; ++i) {
+        const bool more = i + 1 < plan.nb;
+        if (more) gload(qplan_block(plan, i + 1));
+        if (!SINK && i == 0) refill();
+        compute_block(qplan_block(plan, i), lds + (i & 1) * BUF);
+        if (SINK && i == 0) refill();
+        if (more) sstore((i + 1) & 1);
+        __syncthreads();
+      }
     }
     if (plan.nb == 0) refill();  // no key block (cannot happen for valid masks; kept for safety)
     // the next tile's stash has landed (waited here, before this tile's dQ stores, which would

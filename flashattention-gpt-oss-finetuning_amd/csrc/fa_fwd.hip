@@ -458,7 +458,9 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   const EdgeOffsets eo = edge_offsets(W);
 
   int tile = t_lo + pos;
-  if (kStash && tile < t_hi) {
+  const int first_tile = tile;
+  // (PRE loads the first tile's Q rows in the loop, in the same round trip as its key blocks)
+  if (kStash && !PRE && tile < t_hi) {
     stash_rows(decode(tile));
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
@@ -473,17 +475,20 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // after the key loop) or from memory: lane (q, hf) holds head-dim slice [hf*D/2 + 8ks, +8) in
   // step ks.
   u32x4 qf[HPW][KS];
+  auto read_q = [&]() {
 #pragma unroll
-  for (int h = 0; h < HPW; ++h) {
-    if constexpr (kStash) {
+    for (int h = 0; h < HPW; ++h) {
+      if constexpr (kStash) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qf[h][ks] = lds16(stash + (h * KS + ks) * 512 + 8 * lane) ^ a.qsign;
-    } else {
-      const rsrc_t rq = q_rsrc(t, h);
+        for (int ks = 0; ks < KS; ++ks) qf[h][ks] = lds16(stash + (h * KS + ks) * 512 + 8 * lane) ^ a.qsign;
+      } else {
+        const rsrc_t rq = q_rsrc(t, h);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qf[h][ks] = buf_ld16(rq, q_off(t, ks)) ^ a.qsign;
+        for (int ks = 0; ks < KS; ++ks) qf[h][ks] = buf_ld16(rq, q_off(t, ks)) ^ a.qsign;
+      }
     }
-  }
+  };
+  if (!PRE) read_q();
 
   float m2[HPW], lsum[HPW];
   f32x16 acc[HPW][DB];
@@ -579,9 +584,23 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
         else buf_dma16(rk, dst, off);
       }
     };
+    if (plan.nb == 0) {  // no key block: the Q rows are still read out of the stash
+      if (kStash && tile == first_tile) {
+        stash_rows(t);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      read_q();
+    }
     for (int g0 = 0; g0 < plan.nb; g0 += NBUF) {
       const int ng = min(NBUF, plan.nb - g0);
       for (int j = 0; j < ng; ++j) dma_block(qplan_block(plan, g0 + j), j);
+      if (g0 == 0) {
+        if (kStash && tile == first_tile) {  // the first tile's Q rows, with its first blocks
+          stash_rows(t);
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        read_q();
+      }
       // the next tile's Q rows into the stash, once this tile's have been read out of it
       const bool stash_now = kStash && g0 == 0 && tile + wgs_x < t_hi;
       if (stash_now) {
