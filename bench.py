@@ -265,6 +265,45 @@ def time_steps(fa, cfg, q, k, v, do, steps, warmup):
                 bwd_ms=b_ms, peak_mem_gb=peak_gb)
 
 
+def graph_step_measure(fa, cfg, q, k, v, do, steps):
+    """The fwd+bwd step captured once in a HIP graph (torch.cuda.CUDAGraph) and replayed: the
+    time per replay, with no per-step host work (autograd and the launches are recorded once).
+    A finetuning loop whose step is launch-bound can run its attention this way."""
+    import torch
+
+    qg, kg, vg = (t.detach().clone().requires_grad_() for t in (q, k, v))
+    W, S = cfg["W"], cfg["S"]
+
+    def step():
+        fa.flash_swda_with_sink(qg, kg, vg, W, S).backward(do)
+
+    side = torch.cuda.Stream()  # warm-up on a side stream, as capture requires
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            qg.grad = kg.grad = vg.grad = None
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    qg.grad = kg.grad = vg.grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(10):
+        graph.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    flops = _mod("flops").Workload(cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"], cfg["D"], W, S).flops("fwdbwd")
+    return {"ms_per_step": round(ms, 4), "event_ms_per_step": round(ev0.elapsed_time(ev1) / steps, 4),
+            "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s"}
+
+
 VARLEN_SEQS = (4096, 2048, 1024, 512, 3000, 1500, 700, 3504)  # 16384 packed rows
 
 
@@ -634,12 +673,20 @@ def main():
         "kernels": kernels,
         "roofline": roofline,
     }
+    if not args.no_extras:
+        line["graph_step"] = graph_step_measure(fa, cfg, q, k, v, do, args.steps)
     if args.config == "c2" and not args.no_extras:
         line["varlen"] = varlen_measure(args.steps, args.warmup)
         line["shard_proxy"] = sp = shard_proxy_measure(args.steps, args.warmup)
         full = fb_flops / (sum(kt["avg_us"] for kt in line["kernels"].values()) * 1e-6) / 1e12
         sp["per_gpu_vs_full"] = round(sp["value"] / full, 3)  # device throughput, share vs full shape
         line["fp8_forward"] = fp8_forward_measure()
+        # the README shape, whose autograd step is bound by host work: eager and graph-replayed
+        c1 = CONFIGS["c1"]
+        q1, k1, v1, do1 = make_inputs(c1, dev)
+        t1 = time_steps(fa, c1, q1, k1, v1, do1, args.steps, args.warmup)
+        line["c1_step"] = {"workload": "c1: " + c1["name"] + ", fwd+bwd", "eager_ms_per_step": round(t1["fwdbwd_ms"], 4),
+                           "graph": graph_step_measure(fa, c1, q1, k1, v1, do1, args.steps)}
     if not args.no_sdpa_baseline:
         line["sdpa_baseline"] = sdpa_baseline(cfg, q, k, v, do)
     if not args.no_cpu_baseline:
