@@ -10,8 +10,13 @@ The cases walk the edges of its LDS ring and of the sink paths around it:
   * two KV heads, two batches, and G = 16 (two workgroups' head groups per KV head);
   * learned sink logits and packed batches with short and empty sequences (workgroups with no
     tile, which the fold skips).
+  * a seeded random sweep inside the kernels' range, with softmax scales of either sign and zero
+    (a negative scale flips the sign of Q on its way into the products; zero makes every allowed
+    key equally likely).
 Oracles and tolerances as tests/test_gpu_parity.py, test_gpu_sinks.py and test_gpu_varlen.py.
 """
+import random
+
 import pytest
 import torch
 
@@ -59,3 +64,45 @@ def test_slide_learned_sinks(gpu, L, W, S, dtype):
 ])
 def test_slide_varlen(gpu, cu, W, S, sinks):
     run_varlen(cu, 8, 1, 64, W, S, BF, seed=3, sinks=sinks)
+
+
+def _slide_random_cases(n=24, seed=77):
+    """Shapes drawn from a fixed seed inside the sliding kernels' range (D = 64, G a multiple of 8,
+    1 <= W <= 161, S <= 32; the sliding forward takes W <= 129): lengths 1-2500, one or two batches
+    and KV heads, G = 8 or 16, both dtypes, scales of either sign around 1/sqrt(D)."""
+    rng = random.Random(seed)
+    cases = []
+    while len(cases) < n:
+        G = rng.choice([8, 8, 16])
+        Hkv = rng.choice([1, 2])
+        B = rng.choice([1, 1, 2])
+        L = rng.choice([rng.randint(1, 100), rng.randint(101, 1000), rng.randint(1001, 2500)])
+        W = rng.choice([1, rng.randint(2, 129), rng.randint(130, 161)])
+        S = rng.choice([0, rng.randint(1, 8), rng.randint(9, 32)])
+        if B * Hkv * G * L * L > (1 << 27):
+            continue
+        dtype = rng.choice([BF, FP])
+        scale = rng.choice([1.0, 1.0, 1.0, -1.0]) * rng.uniform(0.5, 1.5) / 8.0
+        cases.append(pytest.param(B, Hkv * G, Hkv, L, W, S, dtype, scale, len(cases),
+                                  id=f"SR{len(cases)}-B{B}-H{Hkv * G}x{Hkv}-L{L}-W{W}-S{S}-"
+                                     f"{'bf16' if dtype is BF else 'fp16'}-{'neg' if scale < 0 else 'pos'}"))
+    return cases
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,W,S,dtype,scale,seed", _slide_random_cases())
+def test_slide_random(gpu, B, Hq, Hkv, L, W, S, dtype, scale, seed):
+    """Every case also runs the reference's naive 16-bit path (on the CPU), whose error widens the
+    absolute tolerance as in tests/test_gpu_parity.py.  The dK/dV rows of sink keys sum G x L terms
+    (up to 16 heads x 2500 rows here, values up to about 20), and the 16-bit rounding of P -- in
+    the products and in the forward's row sums, which the LSE carries into the backward -- moves
+    them by a few 1e-2: for the case SR16 an emulation of exactly that rounding in float32
+    reproduces the kernel's dV of the sink keys to half a bf16 ulp, and sits 0.024 from the
+    float32 oracle on one element."""
+    print(f"slide random case B={B} Hq={Hq} Hkv={Hkv} L={L} W={W} S={S} {dtype} scale={scale:.4g}", flush=True)
+    run_case(B, Hq, Hkv, L, 64, W, S, dtype, seed=500 + seed, scale=scale, with_naive=True)
+
+
+@pytest.mark.parametrize("scale", [0.0, -0.125])
+def test_slide_scale_edge(gpu, scale):
+    print(f"slide case scale={scale}", flush=True)
+    run_case(1, 8, 1, 777, 64, 128, 4, BF, seed=9, scale=scale)
