@@ -8,9 +8,12 @@ The cases walk its edges:
   * sink keys in dq_sink_mode (S <= 16 with rows past key block 0's window: the dQ kernel takes
     those rows, and key block 0's workgroup folds the partials), and S = 40 with every row inside
     the window (the sink keys span two 32-key workgroups, whose rows run to L);
-  * packed batches with short and empty sequences, with learned sink logits.
+  * packed batches with short and empty sequences, with learned sink logits;
+  * a seeded random sweep inside its range, with scales of either sign.
 Oracles and tolerances as tests/test_gpu_parity.py, test_gpu_sinks.py and test_gpu_varlen.py.
 """
+import random
+
 import pytest
 
 from test_gpu_parity import BF, FP, run_case
@@ -52,3 +55,34 @@ def test_dkdv4_learned_sinks(gpu):
 def test_dkdv4_varlen(gpu, cu, D, W, S, sinks):
     print(f"case varlen cu={cu} D={D} W={W} S={S} sinks={sinks}", flush=True)
     run_varlen(cu, 8, 2, D, W, S, BF, seed=13, sinks=sinks)
+
+
+def _dkdv4_random_cases(n=16, seed=404):
+    """Shapes drawn from a fixed seed inside the kernel's range: D 16-64, G = 4-16 (a multiple of 4),
+    W 1-512, S 0-16 (sinks past the window go through the dQ kernel), grids of at most 256 key
+    blocks of 64 (so that the kernel, not the 64-key one, runs on a 256-CU device), both dtypes,
+    scales of either sign.  The naive 16-bit path runs too, for the sink keys' widened tolerance."""
+    rng = random.Random(seed)
+    cases = []
+    while len(cases) < n:
+        D = rng.choice([16, 32, 64, 64])
+        G = rng.choice([4, 8, 12, 16])
+        Hkv = rng.choice([1, 2])
+        B = rng.choice([1, 1, 2])
+        L = rng.choice([rng.randint(1, 64), rng.randint(65, 600), rng.randint(601, 1500)])
+        W = rng.choice([1, rng.randint(2, 128), rng.randint(129, 512)])
+        S = rng.choice([0, rng.randint(1, 4), rng.randint(5, 16)])
+        if B * Hkv * ((L + 63) // 64) > 256 or B * Hkv * G * L * L > (1 << 25):
+            continue
+        dtype = rng.choice([BF, FP])
+        scale = rng.choice([1.0, 1.0, -1.0]) * rng.uniform(0.5, 1.5) / D ** 0.5
+        cases.append(pytest.param(B, Hkv * G, Hkv, L, D, W, S, dtype, scale, len(cases),
+                                  id=f"K{len(cases)}-B{B}-H{Hkv * G}x{Hkv}-L{L}-D{D}-W{W}-S{S}-"
+                                     f"{'bf16' if dtype is BF else 'fp16'}-{'neg' if scale < 0 else 'pos'}"))
+    return cases
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,D,W,S,dtype,scale,seed", _dkdv4_random_cases())
+def test_dkdv4_random(gpu, B, Hq, Hkv, L, D, W, S, dtype, scale, seed):
+    print(f"dkdv4 random case B={B} Hq={Hq} Hkv={Hkv} L={L} D={D} W={W} S={S} {dtype} scale={scale:.4g}", flush=True)
+    run_case(B, Hq, Hkv, L, D, W, S, dtype, seed=700 + seed, scale=scale, with_naive=True)
