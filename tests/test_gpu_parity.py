@@ -260,6 +260,34 @@ def test_backward_is_deterministic(gpu):
             assert torch.equal(a, b)
 
 
+# One shape per backward path, each run three more times and compared bitwise: the kernels add
+# partial sums in a fixed order and use no atomics, whichever path the C ABI picks.
+DETERMINISM_CASES = [
+    pytest.param(1, 64, 8, 4096, 64, 128, 4, BF, id="c2-slide-dq-64key-dkdv"),
+    pytest.param(1, 8, 2, 2048, 64, 2048, 0, BF, id="full-causal-generic-dq"),
+    pytest.param(2, 8, 2, 1024, 128, 256, 16, FP, id="D128-sink-rows-in-dq"),
+    pytest.param(1, 16, 16, 2048, 16, 256, 4, FP, id="D16-G1"),
+    pytest.param(1, 8, 2, 1500, 64, 64, 40, BF, id="S40-chunks-and-fold"),
+    pytest.param(1, 4, 2, 600, 64, 100, 4, torch.float32, id="float32"),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,D,W,S,dtype", DETERMINISM_CASES)
+def test_backward_is_deterministic_per_path(gpu, B, Hq, Hkv, L, D, W, S, dtype):
+    print(f"determinism case B={B} Hq={Hq} Hkv={Hkv} L={L} D={D} W={W} S={S} {dtype}", flush=True)
+    ops = load_mod("_ops")
+    q, k, v, do = make_inputs(B, Hq, Hkv, L, D, dtype, seed=19)
+    sc = 1.0 / math.sqrt(D)
+    o, lse = ops.forward(q, k, v, W, S, sc)
+    first = ops.backward(q, k, v, o, lse, do, W, S, sc)
+    for _ in range(3):
+        o2, lse2 = ops.forward(q, k, v, W, S, sc)
+        assert torch.equal(o, o2) and torch.equal(lse, lse2)
+        again = ops.backward(q, k, v, o, lse, do, W, S, sc)
+        for name, a, b in zip(("dQ", "dK", "dV"), first, again):
+            assert torch.equal(a, b), f"{name} differs between two identical calls"
+
+
 def test_error_behaviour_on_gpu(gpu):
     fa = load_pkg()
     q, k, v, _ = make_inputs(1, 4, 2, 64, 64, BF, seed=1)
