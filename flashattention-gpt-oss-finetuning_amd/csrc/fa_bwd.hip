@@ -84,7 +84,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   const int r32 = lane & 31, hf = lane >> 5;
   const int W = a.W, S = a.S;
 
-  // this workgroup's tiles: its XCD's range [t_lo, t_hi), from pos with stride wgs_x
+  // this workgroup's tiles: its XCD's range [t_lo, t_hi), walked in rounds of wgs_x consecutive
+  // tiles, one per workgroup.  Without sink rows, round r gives workgroup pos the tile pos for even
+  // r and wgs_x - 1 - pos for odd r, which evens out the work of causal tiles (it grows with the
+  // row); with sink rows the order stays pos in every round (a stride of wgs_x), which the runs of
+  // sink partials and bwd_sink_fold_kernel rely on.
   const int groups = a.B * a.Hq / a.wh;
   const int n_tiles = a.n_qtiles * groups;
   const int xcd = blockIdx.x % NX, pos = blockIdx.x / NX, wgs_x = gridDim.x / NX;
@@ -174,21 +178,25 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   }
   uint16_t* ptile = SINK ? (D >= 32 ? stash + 2 * TILE : lds + NBUF * BUF + 4 * STASH + wave * 1024) : nullptr;
 
-  int tile = t_lo + pos;
-  int run_first = tile;  // first tile of the current run of tiles of one (batch, KV head)
+  auto tile_of = [&](int r) { return t_lo + r * wgs_x + ((!SINK && (r & 1)) ? wgs_x - 1 - pos : pos); };
+  const int first_tile = tile_of(0);
+  int run_first = first_tile;  // first tile of the current run of tiles of one (batch, KV head)
   float lse_next = 0.f;
-  const int first_tile = tile;
-  if (!PRE && tile < t_hi) {
-    const TileIdx t0 = decode(tile);
+  if (!PRE && first_tile < t_hi) {
+    const TileIdx t0 = decode(first_tile);
     stash_rows(t0);
     lse_next = load_lse(t0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
-  for (; tile < t_hi; tile += wgs_x) {
+  for (int r = 0; t_lo + r * wgs_x < t_hi; ++r) {
+    const int tile = tile_of(r);
+    if (tile >= t_hi) continue;  // the last round is short
+    // the workgroup's next tile (the round after a short last round does not exist)
+    const int next_tile = tile_of(r + 1);
+    const bool has_next = next_tile < t_hi;
     const TileIdx t = decode(tile);
     const int qw = t.qw, q = qw + r32, L = t.L;
     const bool wave_active = qw < L;
-    const bool has_next = tile + wgs_x < t_hi;
 
     const QPlan plan = qplan(t.q0, 32 * a.wq, L, W, S);
     KArgs& Akv = args_fresh();
@@ -292,7 +300,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
     auto refill = [&]() {
       if (has_next) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        const TileIdx tn = decode(tile + wgs_x);
+        const TileIdx tn = decode(next_tile);
         stash_rows(tn);
         lse_next = load_lse(tn);
       }
@@ -466,7 +474,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
       // slot of the run's first tile.  A workgroup has at most one run per (batch, KV head), and
       // the runs of one XCD start at the first wgs_x tiles of its share of that (batch, KV head),
       // which is how bwd_sink_fold_kernel finds the slots.
-      const bool flush = !has_next || (tile + wgs_x) / tiles_per_kv != tile / tiles_per_kv;
+      const bool flush = !has_next || next_tile / tiles_per_kv != tile / tiles_per_kv;
       if (flush) {
         KArgs& A = args_fresh();
         const int sr = A.srows;
@@ -485,7 +493,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
         __syncthreads();
         const int n_out = 2 * sr * D;
         float* slot = A.dq_sink_part + int64_t(run_first) * n_out;
-        run_first = tile + wgs_x;
+        run_first = next_tile;
         for (int x = tid; x < n_out; x += 256) {
           const int kind = x / (sr * D), rest = x % (sr * D);
           float v = 0.f;

@@ -378,8 +378,11 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   const int r32 = lane & 31, hf = lane >> 5;
   const int W = a.W, S = a.S;
 
-  // this workgroup's tiles: its XCD's contiguous range [t_lo, t_hi), from pos with stride
-  // wgs_x (neighbouring tiles share K/V rows in that XCD's L2)
+  // this workgroup's tiles: its XCD's contiguous range [t_lo, t_hi), walked in rounds of wgs_x
+  // consecutive tiles, one per workgroup (neighbouring tiles share K/V rows in that XCD's L2).
+  // Round r gives workgroup pos the tile pos for even r and wgs_x - 1 - pos for odd r: a causal
+  // tile's work grows with its row, and the alternation gives every workgroup about the same sum
+  // (with a fixed stride the last workgroup of an XCD got 1.66x the first's at full causal).
   const int hwg = HPW * a.wh;
   const int n_tiles = a.n_qtiles * a.B * (a.Hq / hwg);
   const int xcd = blockIdx.x % NX, pos = blockIdx.x / NX, wgs_x = gridDim.x / NX;
@@ -457,14 +460,19 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   fwd_patterns(pat, W, S);
   const EdgeOffsets eo = edge_offsets(W);
 
-  int tile = t_lo + pos;
-  const int first_tile = tile;
+  const int first_tile = t_lo + pos;
+  // from a round's tile to the next round's: 2 wgs_x - 1 - 2 pos after an even round, 2 pos + 1
+  // after an odd one
+  int step = 2 * wgs_x - 1 - 2 * pos;
   // (PRE loads the first tile's Q rows in the loop, in the same round trip as its key blocks)
-  if (kStash && !PRE && tile < t_hi) {
-    stash_rows(decode(tile));
+  if (kStash && !PRE && first_tile < t_hi) {
+    stash_rows(decode(first_tile));
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
-  for (; tile < t_hi; tile += wgs_x) {
+  // Only the last round can be short, so the first tile past the range ends the walk.
+  for (int tile = first_tile; tile < t_hi; tile += step, step = 2 * wgs_x - step) {
+  const int next_tile = tile + step;
+  const bool has_next = next_tile < t_hi;
   const TileIdx t = decode(tile);
   const int b = t.b, kvh = t.kvh, hw = t.hw, q0 = t.q0, qw = t.qw, L = t.L;
   const int BM = 32 * a.wq;
@@ -602,10 +610,10 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
         read_q();
       }
       // the next tile's Q rows into the stash, once this tile's have been read out of it
-      const bool stash_now = kStash && g0 == 0 && tile + wgs_x < t_hi;
+      const bool stash_now = kStash && g0 == 0 && has_next;
       if (stash_now) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        stash_rows(decode(tile + wgs_x));
+        stash_rows(decode(next_tile));
         wait_vm_lgkm0_barrier<HPW * KS>();  // the blocks have landed (the stash may be in flight)
       } else {
         wait_vm_lgkm0_barrier<0>();
@@ -623,18 +631,18 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
       const bool more = i + 1 < plan.nb;
       if (more) gload(qplan_block(plan, i + 1));
       // the next tile's Q rows into the stash, once this tile's have been read out of it
-      if (kStash && i == 0 && tile + wgs_x < t_hi) {
+      if (kStash && i == 0 && has_next) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        stash_rows(decode(tile + wgs_x));
+        stash_rows(decode(next_tile));
       }
       compute_block(qplan_block(plan, i), i & 1);
       if (more) sstore((i + 1) & 1);
       __syncthreads();
     }
   }
-  if (kStash && plan.nb == 0 && tile + wgs_x < t_hi) {  // no key block: stash it here
+  if (kStash && plan.nb == 0 && has_next) {  // no key block: stash it here
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    stash_rows(decode(tile + wgs_x));
+    stash_rows(decode(next_tile));
   }
   // the next tile's stash has landed (waited here, before this tile's O stores, which would
   // otherwise also be waited for)
