@@ -188,6 +188,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
     lse_next = load_lse(t0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
+  // (A round counter rather than the forward's step: with the step, the D = 128 variant with sink
+  // rows, at its register limit, waited for a load one block earlier, 3% more at c5.)
   for (int r = 0; t_lo + r * wgs_x < t_hi; ++r) {
     const int tile = tile_of(r);
     if (tile >= t_hi) continue;  // the last round is short
