@@ -1,0 +1,71 @@
+"""GPU parity at GPT-OSS's 128K context with tensors past 2^32 bytes.
+
+B = 5, Hq = 64, Hkv = 8, L = 131072, D = 64, bf16: q, o, dO and dQ are 5.4 GB each, so the
+(batch, head) slices of the last batches start past 2^31 and 2^32 bytes, where a 32-bit base
+offset would wrap.  Two configurations cover both kernel families: the sliding kernels
+(W = 128, S = 4, sink rows in the dQ kernel) and the generic ones (W = 300, S = 40, sink keys
+in chunk workgroups and the fold).
+
+The float32 oracle cannot run the whole problem, so each sample of 64 rows [r0, r0 + 64) of one
+sequence is checked against the oracle on a sub-problem: the S sink keys followed by positions
+[t0, r0 + 64), t0 = r0 - W - 64.  Differences of positions inside the tail are kept and the sinks
+stay the first S keys, so the sampled rows see exactly the keys they see in the full sequence
+(every key they can reach lies at or past r0 - W + 1 > t0).  Their O, LSE and dQ must therefore
+agree; at the end of a sequence (r0 = L - 64) every row that reaches the last 64 keys is sampled,
+so those keys' dK and dV must agree too.  Every head is checked, at test_gpu_parity.py's bar.
+"""
+import math
+
+import pytest
+import torch
+
+from conftest import load_mod
+from oracle import naive
+from test_gpu_parity import assert_close
+
+pytestmark = pytest.mark.gpu
+
+B, HQ, HKV, L, D = 5, 64, 8, 131072, 64
+
+
+def subproblem_keys(r0, W, S):
+    """Positions of the sub-problem for rows [r0, r0 + 64): the S sinks, then [r0 - W - 64, r0 + 64)."""
+    t0 = r0 - W - 64
+    assert t0 >= S
+    return torch.cat([torch.arange(S), torch.arange(t0, r0 + 64)])
+
+
+def _randn(shape, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return torch.randn(shape, device="cuda", dtype=torch.bfloat16, generator=g)
+
+
+@pytest.mark.parametrize("W,S", [pytest.param(128, 4, id="sliding-kernels"),
+                                 pytest.param(300, 40, id="generic-kernels-sink-chunks")])
+def test_long_context_past_4gb(gpu, W, S):
+    ops = load_mod("_ops")
+    print(f"case B={B} Hq={HQ} Hkv={HKV} L={L} D={D} W={W} S={S} bf16", flush=True)
+    q = _randn((B, HQ, L, D), 1)
+    k, v = _randn((B, HKV, L, D), 2), _randn((B, HKV, L, D), 3)
+    do = _randn((B, HQ, L, D), 4)
+    assert q.numel() * q.element_size() > 1 << 32
+    sc = 1.0 / math.sqrt(D)
+    o, lse = ops.forward(q, k, v, W, S, sc)
+    dq, dk, dv = ops.backward(q, k, v, o, lse, do, W, S, sc)
+    torch.cuda.synchronize()
+    for b, r0 in ((B - 1, L - 64), (B - 1, L // 2 + 13), (3, 100000), (0, 4096)):
+        idx = subproblem_keys(r0, W, S).cuda()
+        sub = lambda t: t[b:b + 1].index_select(2, idx).contiguous()
+        ro, rlse, rdq, rdk, rdv = naive.attention_fwd_bwd(sub(q), sub(k), sub(v), sub(do), W, S, scale=sc,
+                                                          compute_dtype=torch.float32)
+        n = idx.numel()
+        rows = slice(r0, r0 + 64)
+        tag = f"b={b} rows {r0}-{r0 + 63}"
+        assert_close(f"O {tag}", o[b, :, rows], ro[0, :, n - 64:])
+        assert_close(f"LSE {tag}", lse[b, :, rows], rlse[0, :, n - 64:])
+        assert_close(f"dQ {tag}", dq[b, :, rows], rdq[0, :, n - 64:])
+        if r0 + 64 == L:
+            assert_close(f"dK {tag}", dk[b, :, rows], rdk[0, :, n - 64:])
+            assert_close(f"dV {tag}", dv[b, :, rows], rdv[0, :, n - 64:])
+    del q, k, v, do, o, lse, dq, dk, dv
+    torch.cuda.empty_cache()

@@ -178,3 +178,26 @@ def test_naive_reference_dtype_path_close_to_fp64():
         o = naive.naive_attention(q.to(dt), k.to(dt), v.to(dt), 16, 4)
         assert o.dtype == dt
         assert (o.double() - o64).abs().max() < 5e-2
+
+
+@pytest.mark.parametrize("L,W,S,r0", [(900, 128, 4, 836), (900, 128, 4, 413), (1000, 300, 40, 936),
+                                      (1000, 300, 40, 500)])
+def test_long_context_subproblem_is_exact(L, W, S, r0):
+    """The sub-problem tests/test_gpu_long.py checks sampled rows with (the S sinks, then
+    positions [r0 - W - 64, r0 + 64)) gives those rows the same O, LSE and dQ as the whole
+    sequence, and at the sequence's end the last 64 keys the same dK and dV."""
+    from test_gpu_long import subproblem_keys
+
+    q, k, v, do = _inputs(1, 4, 2, L, 8, seed=r0)
+    full = naive.attention_fwd_bwd(q, k, v, do, W, S, compute_dtype=torch.float64)
+    idx = subproblem_keys(r0, W, S)
+    sub = naive.attention_fwd_bwd(*(t.index_select(2, idx) for t in (q, k, v, do)), W, S,
+                                  compute_dtype=torch.float64)
+    n, rows = idx.numel(), slice(r0, r0 + 64)
+    for i in (0, 1, 2):  # O, LSE, dQ
+        torch.testing.assert_close(sub[i][:, :, n - 64:], full[i][:, :, rows])
+    if r0 + 64 == L:
+        for i in (3, 4):  # dK, dV
+            torch.testing.assert_close(sub[i][:, :, n - 64:], full[i][:, :, rows])
+    else:  # away from the end, the keys also get gradient from rows past the sample
+        assert not torch.allclose(sub[3][:, :, n - 64:], full[3][:, :, rows])
