@@ -4,7 +4,8 @@ B = 5, Hq = 64, Hkv = 8, L = 131072, D = 64, bf16: q, o, dO and dQ are 5.4 GB ea
 (batch, head) slices of the last batches start past 2^31 and 2^32 bytes, where a 32-bit base
 offset would wrap.  Two configurations cover both kernel families: the sliding kernels
 (W = 128, S = 4, sink rows in the dQ kernel) and the generic ones (W = 300, S = 40, sink keys
-in chunk workgroups and the fold).
+in chunk workgroups and the fold).  The sliding one runs again in the [B, L, H, D] layout, where
+one head's slice spans 1 GB.
 
 The float32 oracle cannot run the whole problem, so each sample of 64 rows [r0, r0 + 64) of one
 sequence is checked against the oracle on a sub-problem: the S sink keys followed by positions
@@ -35,19 +36,24 @@ def subproblem_keys(r0, W, S):
     return torch.cat([torch.arange(S), torch.arange(t0, r0 + 64)])
 
 
-def _randn(shape, seed):
+def _randn(B, H, seed, layout):
+    """A [B, H, L, D] bf16 tensor, or a [B, H, L, D] view of a [B, L, H, D] one (GPT-OSS's layout:
+    each head's rows are H * D elements apart, so a head's slice spans 1 GB here)."""
     g = torch.Generator(device="cuda").manual_seed(seed)
-    return torch.randn(shape, device="cuda", dtype=torch.bfloat16, generator=g)
+    if layout == "blhd":
+        return torch.randn((B, L, H, D), device="cuda", dtype=torch.bfloat16, generator=g).transpose(1, 2)
+    return torch.randn((B, H, L, D), device="cuda", dtype=torch.bfloat16, generator=g)
 
 
-@pytest.mark.parametrize("W,S", [pytest.param(128, 4, id="sliding-kernels"),
-                                 pytest.param(300, 40, id="generic-kernels-sink-chunks")])
-def test_long_context_past_4gb(gpu, W, S):
+@pytest.mark.parametrize("W,S,layout", [pytest.param(128, 4, "bhld", id="sliding-kernels"),
+                                        pytest.param(300, 40, "bhld", id="generic-kernels-sink-chunks"),
+                                        pytest.param(128, 4, "blhd", id="sliding-kernels-BLHD-layout")])
+def test_long_context_past_4gb(gpu, W, S, layout):
     ops = load_mod("_ops")
-    print(f"case B={B} Hq={HQ} Hkv={HKV} L={L} D={D} W={W} S={S} bf16", flush=True)
-    q = _randn((B, HQ, L, D), 1)
-    k, v = _randn((B, HKV, L, D), 2), _randn((B, HKV, L, D), 3)
-    do = _randn((B, HQ, L, D), 4)
+    print(f"case B={B} Hq={HQ} Hkv={HKV} L={L} D={D} W={W} S={S} bf16 {layout}", flush=True)
+    q = _randn(B, HQ, 1, layout)
+    k, v = _randn(B, HKV, 2, layout), _randn(B, HKV, 3, layout)
+    do = _randn(B, HQ, 4, layout)
     assert q.numel() * q.element_size() > 1 << 32
     sc = 1.0 / math.sqrt(D)
     o, lse = ops.forward(q, k, v, W, S, sc)
