@@ -75,3 +75,44 @@ def test_long_context_past_4gb(gpu, W, S, layout):
             assert_close(f"dV {tag}", dv[b, :, rows], rdv[0, :, n - 64:])
     del q, k, v, do, o, lse, dq, dk, dv
     torch.cuda.empty_cache()
+
+
+def test_long_packed_batch(gpu):
+    """A packed batch of 200000 rows: a 128K-row sequence, a 1-row one, then 8927 and 60000 rows,
+    Hq = 64, Hkv = 8, D = 64, W = 128, S = 4, bf16.  Each head's slice spans the whole packed
+    tensor (1.6 GB).  Sampled rows are checked on the same sub-problems, built from each
+    sequence's own positions; the 1-row sequence is checked whole."""
+    ops = load_mod("_ops")
+    W, S = 128, 4
+    cu = [0, 131072, 131073, 140000, 200000]
+    total = cu[-1]
+    print(f"case packed cu={cu} Hq={HQ} Hkv={HKV} D={D} W={W} S={S} bf16", flush=True)
+    mk = lambda H, seed: torch.randn((total, H, D), device="cuda", dtype=torch.bfloat16,
+                                     generator=torch.Generator(device="cuda").manual_seed(seed))
+    q, k, v, do = mk(HQ, 11), mk(HKV, 12), mk(HKV, 13), mk(HQ, 14)
+    sc = 1.0 / math.sqrt(D)
+    cu_dev, max_len = ops.cu_seqlens_ready(torch.tensor(cu, dtype=torch.int32), total, q.device)
+    o, lse = ops.forward_varlen(q, k, v, cu_dev, max_len, W, S, sc)
+    dq, dk, dv = ops.backward_varlen(q, k, v, o, lse, do, cu_dev, max_len, W, S, sc)
+    torch.cuda.synchronize()
+    # (sequence, first sampled row relative to its start; None: the whole sequence)
+    for s, r0 in ((0, 131072 - 64), (0, 70001), (1, None), (2, 8927 - 64), (3, 33333)):
+        lo, n_seq = cu[s], cu[s + 1] - cu[s]
+        idx = torch.arange(n_seq) if r0 is None else subproblem_keys(r0, W, S)
+        rel = slice(0, n_seq) if r0 is None else slice(r0, r0 + 64)
+        rows = torch.arange(rel.start, rel.stop).cuda() + lo
+        pos = idx.cuda() + lo
+        sub = lambda t: t.index_select(0, pos).permute(1, 0, 2).unsqueeze(0).contiguous()
+        ro, rlse, rdq, rdk, rdv = naive.attention_fwd_bwd(sub(q), sub(k), sub(v), sub(do), W, S, scale=sc,
+                                                          compute_dtype=torch.float32)
+        m = rel.stop - rel.start
+        got = lambda t: t.index_select(0, rows).permute(1, 0, 2)
+        tag = f"sequence {s} rows {rel.start}-{rel.stop - 1}"
+        assert_close(f"O {tag}", got(o), ro[0, :, -m:])
+        assert_close(f"LSE {tag}", lse.index_select(1, rows), rlse[0, :, -m:])
+        assert_close(f"dQ {tag}", got(dq), rdq[0, :, -m:])
+        if rel.stop == n_seq:
+            assert_close(f"dK {tag}", got(dk), rdk[0, :, -m:])
+            assert_close(f"dV {tag}", got(dv), rdv[0, :, -m:])
+    del q, k, v, do, o, lse, dq, dk, dv
+    torch.cuda.empty_cache()
