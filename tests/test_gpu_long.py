@@ -5,7 +5,7 @@ B = 5, Hq = 64, Hkv = 8, L = 131072, D = 64, bf16: q, o, dO and dQ are 5.4 GB ea
 offset would wrap.  Two configurations cover both kernel families: the sliding kernels
 (W = 128, S = 4, sink rows in the dQ kernel) and the generic ones (W = 300, S = 40, sink keys
 in chunk workgroups and the fold).  The sliding one runs again in the [B, L, H, D] layout, where
-one head's slice spans 1 GB.
+one head's slice spans 1 GB, and once more as GPT-OSS runs it: learned sink logits and S = 0.
 
 The float32 oracle cannot run the whole problem, so each sample of 64 rows [r0, r0 + 64) of one
 sequence is checked against the oracle on a sub-problem: the S sink keys followed by positions
@@ -45,25 +45,36 @@ def _randn(B, H, seed, layout):
     return torch.randn((B, H, L, D), device="cuda", dtype=torch.bfloat16, generator=g)
 
 
-@pytest.mark.parametrize("W,S,layout", [pytest.param(128, 4, "bhld", id="sliding-kernels"),
-                                        pytest.param(300, 40, "bhld", id="generic-kernels-sink-chunks"),
-                                        pytest.param(128, 4, "blhd", id="sliding-kernels-BLHD-layout")])
-def test_long_context_past_4gb(gpu, W, S, layout):
+@pytest.mark.parametrize("W,S,layout,learned", [
+    pytest.param(128, 4, "bhld", False, id="sliding-kernels"),
+    pytest.param(300, 40, "bhld", False, id="generic-kernels-sink-chunks"),
+    pytest.param(128, 4, "blhd", False, id="sliding-kernels-BLHD-layout"),
+    # GPT-OSS's sliding layer as its model runs it: learned sink logits, no positional sinks
+    pytest.param(128, 0, "blhd", True, id="gpt-oss-learned-sinks-BLHD-layout"),
+])
+def test_long_context_past_4gb(gpu, W, S, layout, learned):
     ops = load_mod("_ops")
-    print(f"case B={B} Hq={HQ} Hkv={HKV} L={L} D={D} W={W} S={S} bf16 {layout}", flush=True)
+    print(f"case B={B} Hq={HQ} Hkv={HKV} L={L} D={D} W={W} S={S} bf16 {layout} learned={learned}", flush=True)
     q = _randn(B, HQ, 1, layout)
     k, v = _randn(B, HKV, 2, layout), _randn(B, HKV, 3, layout)
     do = _randn(B, HQ, 4, layout)
     assert q.numel() * q.element_size() > 1 << 32
     sc = 1.0 / math.sqrt(D)
-    o, lse = ops.forward(q, k, v, W, S, sc)
-    dq, dk, dv = ops.backward(q, k, v, o, lse, do, W, S, sc)
+    # learned sink logits exact in bf16, about the size of the scores
+    sk = (2.0 * torch.randn(HQ, generator=torch.Generator().manual_seed(5))).to(torch.bfloat16).float().cuda() \
+        if learned else None
+    o, lse = ops.forward(q, k, v, W, S, sc, sinks=sk)
+    dq, dk, dv = ops.backward(q, k, v, o, lse, do, W, S, sc, sinks=sk)[:3]
     torch.cuda.synchronize()
     for b, r0 in ((B - 1, L - 64), (B - 1, L // 2 + 13), (3, 100000), (0, 4096)):
         idx = subproblem_keys(r0, W, S).cuda()
         sub = lambda t: t[b:b + 1].index_select(2, idx).contiguous()
-        ro, rlse, rdq, rdk, rdv = naive.attention_fwd_bwd(sub(q), sub(k), sub(v), sub(do), W, S, scale=sc,
-                                                          compute_dtype=torch.float32)
+        if learned:  # the sink gradient sums every row of a head: not checked on samples
+            ro, rlse, rdq, rdk, rdv, _ = naive.attention_fwd_bwd_sinks(sub(q), sub(k), sub(v), sk, sub(do), W, S,
+                                                                       scale=sc, compute_dtype=torch.float32)
+        else:
+            ro, rlse, rdq, rdk, rdv = naive.attention_fwd_bwd(sub(q), sub(k), sub(v), sub(do), W, S, scale=sc,
+                                                              compute_dtype=torch.float32)
         n = idx.numel()
         rows = slice(r0, r0 + 64)
         tag = f"b={b} rows {r0}-{r0 + 63}"

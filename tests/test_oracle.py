@@ -180,19 +180,23 @@ def test_naive_reference_dtype_path_close_to_fp64():
         assert (o.double() - o64).abs().max() < 5e-2
 
 
-@pytest.mark.parametrize("L,W,S,r0", [(900, 128, 4, 836), (900, 128, 4, 413), (1000, 300, 40, 936),
-                                      (1000, 300, 40, 500)])
-def test_long_context_subproblem_is_exact(L, W, S, r0):
+@pytest.mark.parametrize("L,W,S,r0,learned", [(900, 128, 4, 836, False), (900, 128, 4, 413, False),
+                                              (1000, 300, 40, 936, False), (1000, 300, 40, 500, False),
+                                              (900, 128, 0, 836, True), (900, 128, 0, 300, True)])
+def test_long_context_subproblem_is_exact(L, W, S, r0, learned):
     """The sub-problem tests/test_gpu_long.py checks sampled rows with (the S sinks, then
     positions [r0 - W - 64, r0 + 64)) gives those rows the same O, LSE and dQ as the whole
-    sequence, and at the sequence's end the last 64 keys the same dK and dV."""
+    sequence, and at the sequence's end the last 64 keys the same dK and dV; with learned sink
+    logits as well (they add a term per head to every row, not a key)."""
     from test_gpu_long import subproblem_keys
 
     q, k, v, do = _inputs(1, 4, 2, L, 8, seed=r0)
-    full = naive.attention_fwd_bwd(q, k, v, do, W, S, compute_dtype=torch.float64)
+    sk = torch.randn(4, dtype=torch.float64, generator=torch.Generator().manual_seed(r0))
+    run = (lambda *t: naive.attention_fwd_bwd_sinks(t[0], t[1], t[2], sk, t[3], W, S, compute_dtype=torch.float64)) \
+        if learned else (lambda *t: naive.attention_fwd_bwd(*t, W, S, compute_dtype=torch.float64))
+    full = run(q, k, v, do)
     idx = subproblem_keys(r0, W, S)
-    sub = naive.attention_fwd_bwd(*(t.index_select(2, idx) for t in (q, k, v, do)), W, S,
-                                  compute_dtype=torch.float64)
+    sub = run(*(t.index_select(2, idx) for t in (q, k, v, do)))
     n, rows = idx.numel(), slice(r0, r0 + 64)
     for i in (0, 1, 2):  # O, LSE, dQ
         torch.testing.assert_close(sub[i][:, :, n - 64:], full[i][:, :, rows])
