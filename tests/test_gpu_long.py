@@ -127,3 +127,38 @@ def test_long_packed_batch(gpu):
             assert_close(f"dV {tag}", got(dv), rdv[0, :, -m:])
     del q, k, v, do, o, lse, dq, dk, dv
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("fp8_pv", [pytest.param(False, id="fa_fwd_fp8"), pytest.param(True, id="fa_fwd_fp8_pv")])
+def test_long_fp8_forward_past_4gb(gpu, fp8_pv):
+    """The fp8 forwards at 128K context with B = 9, so that the 1-byte q (4.8 GB) and the bf16 o
+    (9.7 GB) both have slices past 2^32 bytes (W = 128, S = 4).  Sampled rows are checked on the
+    sub-problems above with test_gpu_fp8.py's bars: the oracle on the dequantised inputs at the
+    16-bit bar for fa_fwd_fp8, and the bound that rounding P to e4m3 allows for fa_fwd_fp8_pv."""
+    from test_gpu_fp8 import assert_pv_close, pv_bound, reference
+
+    ops = load_mod("_ops")
+    Bf, W, S = 9, 128, 4
+    print(f"case fp8 B={Bf} Hq={HQ} Hkv={HKV} L={L} D={D} W={W} S={S} fp8_pv={fp8_pv}", flush=True)
+    mk = lambda H, seed: torch.randn((Bf, H, L, D), device="cuda", dtype=torch.bfloat16,
+                                     generator=torch.Generator(device="cuda").manual_seed(seed)).to(torch.float8_e4m3fn)
+    q8, k8, v8 = mk(HQ, 21), mk(HKV, 22), mk(HKV, 23)
+    assert q8.numel() > 1 << 32
+    ds = (0.5, 0.25, 1.0)  # q, k, v stand for ds[i] times their e4m3 values
+    sc = 1.0 / math.sqrt(D)
+    o, lse = ops.forward_fp8(q8, k8, v8, W, S, sc, ds, fp8_pv=fp8_pv)
+    torch.cuda.synchronize()
+    for b, r0 in ((Bf - 1, L - 64), (Bf - 1, 70001), (4, 100000), (0, 4096)):
+        idx = subproblem_keys(r0, W, S).cuda()
+        sub = lambda t: t[b:b + 1].view(torch.uint8).index_select(2, idx).contiguous().view(torch.float8_e4m3fn)
+        qs, ks, vs = sub(q8), sub(k8), sub(v8)
+        ro, rlse = reference(qs, ks, vs, ds, W, S, sc)
+        got_o, got_lse = o[b:b + 1, :, r0:r0 + 64], lse[b:b + 1, :, r0:r0 + 64]
+        if fp8_pv:
+            bound, lse_bound = pv_bound(qs, ks, vs, ds, W, S, sc, ro)
+            assert_pv_close(got_o, got_lse, ro[:, :, -64:], rlse[:, :, -64:], bound[:, :, -64:], lse_bound[:, :, -64:])
+        else:
+            assert_close(f"O b={b} rows {r0}-{r0 + 63}", got_o, ro[:, :, -64:])
+            assert_close(f"LSE b={b} rows {r0}-{r0 + 63}", got_lse, rlse[:, :, -64:])
+    del q8, k8, v8, o, lse
+    torch.cuda.empty_cache()
