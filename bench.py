@@ -344,6 +344,43 @@ def varlen_measure(steps, warmup, seqs=VARLEN_SEQS):
             "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s"}
 
 
+def long_context_measure(steps=10, warmup=3, L=131072):
+    """fwd + bwd of GPT-OSS's sliding layer at its 128K context as its model runs it: learned sink
+    logits (with their gradient), no positional sinks, q/k/v in the projections' [B, L, H, D]
+    layout, through the adapter gpt_oss.attention.  B = 1, Hq = 64, Hkv = 8, D = 64, W = 128,
+    bf16; useful FLOPs count the allowed pairs (a learned sink adds no key)."""
+    import torch
+
+    gpt_oss = _mod("gpt_oss")
+    flops_mod = _mod("flops")
+    Hq, Hkv, D, W = 64, 8, 64, 128
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    mk = lambda H: torch.randn(1, L, H, D, device=dev, dtype=torch.bfloat16, generator=g)
+    q, k, v, do = mk(Hq).requires_grad_(), mk(Hkv).requires_grad_(), mk(Hkv).requires_grad_(), mk(Hq)
+    sinks = torch.randn(Hq, device=dev, generator=g).requires_grad_()
+
+    def step():
+        q.grad = k.grad = v.grad = sinks.grad = None
+        o = gpt_oss.attention(q, k, v, window_size=W, sinks=sinks, layout="blhd")
+        o.backward(do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = 14.0 * D * flops_mod.allowed_pairs_per_head(L, W, 0) * Hq
+    return {"workload": f"GPT-OSS sliding layer at {L // 1024}K context: B=1 Hq={Hq} Hkv={Hkv} L={L} D={D} W={W}, "
+                        "learned sinks (and their gradient), [B, L, H, D] layout via gpt_oss.attention, bf16, fwd+bwd",
+            "ms_per_step": round(ms, 4), "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s"}
+
+
 def shard_proxy_measure(steps, warmup, name="c2", parts=8):
     """One GPU's share of `name` split over `parts` GPUs by KV-head groups (zero communication:
     dK/dV reduce only inside a group): the same fwd + bwd on Hq / parts query heads and
@@ -680,6 +717,7 @@ def main():
         line["graph_step"] = graph_step_measure(fa, cfg, q, k, v, do, args.steps)
     if args.config == "c2" and not args.no_extras:
         line["varlen"] = varlen_measure(args.steps, args.warmup)
+        line["long_context"] = long_context_measure()
         line["shard_proxy"] = sp = shard_proxy_measure(args.steps, args.warmup)
         full = fb_flops / (sum(kt["avg_us"] for kt in line["kernels"].values()) * 1e-6) / 1e12
         sp["per_gpu_vs_full"] = round(sp["value"] / full, 3)  # device throughput, share vs full shape

@@ -5,6 +5,7 @@
 // causal only, shape agreement, D <= 128, Hq % Hkv == 0; benchmark_backward_speed.py:476-484)
 // plus what the kernels assume (16-byte aligned rows, D in {16, 32, 64, 128}).  Nothing in
 // fa_check_* touches HIP, so the checks run on machines without a GPU.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -165,16 +166,29 @@ int device_cus() {
   return n;
 }
 
+// 32-row tiles with rows, over the 8-head groups of the sliding kernels' units.  n_qt counts the
+// tiles of the longest sequence; a packed batch has at most ceil(total_rows / 32) + B tiles with
+// rows (each sequence adds at most one partial tile), however long its longest sequence, and the
+// units past a short sequence's end exit at once, so sizing the units by B n_qt would leave the
+// device partly idle (a batch of short sequences beside one long one).
+int64_t slide_tile_slots(const fa::Args& a) {
+  const int64_t n_qt = (int64_t(a.L) + 31) / 32;
+  int64_t tiles = int64_t(a.B) * n_qt;
+  if (a.cu_seqlens) tiles = std::min(tiles, (int64_t(a.total_rows) + 31) / 32 + a.B);
+  return tiles * a.Hkv * (a.G / 8);
+}
+
 // The sliding dQ kernel (fa_bwd_slide.hip) serves D = 64 16-bit backwards whose KV groups hold a
 // multiple of 8 query heads, with a window of 1..161 keys (at most 6 key halves of 32 in LDS) and
 // at most 32 sink keys (one sink half).  Its workgroups take slide_ct consecutive 32-row tiles,
-// sized so that the units about fill the device once.
+// sized so that the units with rows about fill the device once.  (Any slide_ct >= 1 fits the
+// workspace: the units, B Hkv (G / 8) slide_ncu, never exceed half of bwd_dq_kernel's tiles, for
+// which the dQ sink slots are sized.)
 void plan_slide(fa::Args& a, int D) {
   if (D != 64 || a.G % 8 != 0 || a.W < 1 || a.W > fa::kSlideMaxW || a.S > 32 || a.L < 1) return;
   const int64_t n_qt = (int64_t(a.L) + 31) / 32;
-  const int64_t groups = int64_t(a.B) * a.Hkv * (a.G / 8);
   const int64_t cus = device_cus();
-  int64_t ct = (groups * n_qt + cus - 1) / cus;
+  int64_t ct = (slide_tile_slots(a) + cus - 1) / cus;
   if (ct < 1) ct = 1;
   a.dq_slide = 1;
   a.slide_ct = int(ct);
@@ -188,9 +202,8 @@ bool plan_fwd_slide(fa::Args& a, int D, int dtype) {
       a.L < 1)
     return false;
   const int64_t n_qt = (int64_t(a.L) + 31) / 32;
-  const int64_t groups = int64_t(a.B) * a.Hkv * (a.G / 8);
   const int64_t slots = 2 * int64_t(device_cus());
-  int64_t ct = (groups * n_qt + slots - 1) / slots;
+  int64_t ct = (slide_tile_slots(a) + slots - 1) / slots;
   if (ct < 1) ct = 1;
   a.slide_ct = int(ct);
   a.slide_ncu = int((n_qt + ct - 1) / ct);
@@ -565,6 +578,7 @@ int fa_bwd_varlen(const fa_bwd_params* p, const int32_t* cu_seqlens, int32_t tot
   if (!sinks != !dsinks) return FA_ERR_NULL;
   if ((sinks && !aligned4(sinks)) || (dsinks && !aligned4(dsinks))) return FA_ERR_ALIGN;
   set_varlen(&a, cu_seqlens, total_rows);
+  if (a.dq_slide) plan_slide(a, p->head_dim);  // size the units by the rows the batch holds
   a.sink_logits = sinks;
   a.dsink = dsinks;
   const hipStream_t s = static_cast<hipStream_t>(stream);
