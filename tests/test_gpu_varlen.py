@@ -89,6 +89,13 @@ def run_varlen(cu, Hq, Hkv, D, W, S, dtype, seed=0, sinks=False, with_naive=True
     pytest.param([0, 64, 128, 192, 256], 16, 2, 64, 32, 4, BF, id="equal-lengths"),
     pytest.param([0, 0, 1, 1, 2], 2, 1, 64, 8, 1, FP, id="tiny-and-empty"),
     pytest.param([0, 2048, 4096], 64, 8, 64, 128, 4, BF, id="gpt-oss-shape-two-sequences"),
+    # short sequences beside long ones on the sliding kernels, whose units are sized by the rows
+    # the batch holds (not by B x the longest sequence): sink rows in the dQ kernel, then in
+    # chunk workgroups
+    pytest.param([0, 4096, 6144, 7168, 7680, 10680, 12180, 12880, 16384], 64, 8, 64, 128, 4, BF,
+                 id="gpt-oss-eight-mixed-lengths"),
+    pytest.param([0, 4096, 6144, 7168, 7680, 10680, 12180, 12880, 16384], 64, 8, 64, 100, 24, FP,
+                 id="gpt-oss-eight-mixed-lengths-S24"),
 ])
 def test_varlen_parity(gpu, cu, Hq, Hkv, D, W, S, dtype):
     run_varlen(cu, Hq, Hkv, D, W, S, dtype, seed=cu[-1] % 97 + D, with_naive=cu[-1] * Hq <= 1 << 16)
