@@ -166,16 +166,24 @@ int device_cus() {
   return n;
 }
 
-// 32-row tiles with rows, over the 8-head groups of the sliding kernels' units.  n_qt counts the
-// tiles of the longest sequence; a packed batch has at most ceil(total_rows / 32) + B tiles with
-// rows (each sequence adds at most one partial tile), however long its longest sequence, and the
-// units past a short sequence's end exit at once, so sizing the units by B n_qt would leave the
-// device partly idle (a batch of short sequences beside one long one).
-int64_t slide_tile_slots(const fa::Args& a) {
+// Tiles per unit (slide_ct) of the sliding kernels, for `slots` resident units.  A fixed-length
+// batch spreads its B Hkv (G / 8) n_qt tiles evenly over the slots.  A packed batch holds at most
+// T = ceil(total_rows / 32) + B tiles with rows (each sequence adds at most one partial tile),
+// however long its longest sequence (which sets n_qt); units past a short sequence's end exit at
+// once.  Its units cut every sequence separately, so a (KV head, head group of 8) needs about
+// T / ct + B / 2 units (half a unit lost per sequence on average), and ct is raised until those
+// fit the slots: units that spill into a second round would double the kernel's time.
+int slide_units_ct(const fa::Args& a, int64_t slots) {
   const int64_t n_qt = (int64_t(a.L) + 31) / 32;
+  const int64_t hg = int64_t(a.Hkv) * (a.G / 8);
   int64_t tiles = int64_t(a.B) * n_qt;
   if (a.cu_seqlens) tiles = std::min(tiles, (int64_t(a.total_rows) + 31) / 32 + a.B);
-  return tiles * a.Hkv * (a.G / 8);
+  int64_t ct = (hg * tiles + slots - 1) / slots;
+  if (a.cu_seqlens) {
+    const int64_t per_group = slots / hg - a.B / 2;
+    if (per_group >= 1) ct = std::max(ct, (tiles + per_group - 1) / per_group);
+  }
+  return int(std::max<int64_t>(ct, 1));
 }
 
 // The sliding dQ kernel (fa_bwd_slide.hip) serves D = 64 16-bit backwards whose KV groups hold a
@@ -187,9 +195,7 @@ int64_t slide_tile_slots(const fa::Args& a) {
 void plan_slide(fa::Args& a, int D) {
   if (D != 64 || a.G % 8 != 0 || a.W < 1 || a.W > fa::kSlideMaxW || a.S > 32 || a.L < 1) return;
   const int64_t n_qt = (int64_t(a.L) + 31) / 32;
-  const int64_t cus = device_cus();
-  int64_t ct = (slide_tile_slots(a) + cus - 1) / cus;
-  if (ct < 1) ct = 1;
+  const int64_t ct = slide_units_ct(a, device_cus());
   a.dq_slide = 1;
   a.slide_ct = int(ct);
   a.slide_ncu = int((n_qt + ct - 1) / ct);
@@ -202,9 +208,7 @@ bool plan_fwd_slide(fa::Args& a, int D, int dtype) {
       a.L < 1)
     return false;
   const int64_t n_qt = (int64_t(a.L) + 31) / 32;
-  const int64_t slots = 2 * int64_t(device_cus());
-  int64_t ct = (slide_tile_slots(a) + slots - 1) / slots;
-  if (ct < 1) ct = 1;
+  const int64_t ct = slide_units_ct(a, 2 * int64_t(device_cus()));
   a.slide_ct = int(ct);
   a.slide_ncu = int((n_qt + ct - 1) / ct);
   return true;
