@@ -243,15 +243,19 @@ def time_steps(fa, cfg, q, k, v, do, steps, warmup):
         for _ in range(warmup):
             fa.flash_swda_with_sink(q, k, v, W, S)
         torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
         t0 = time.perf_counter()
         for _ in range(steps):
             fa.flash_swda_with_sink(q, k, v, W, S)
         torch.cuda.synchronize()
         f_ms = (time.perf_counter() - t0) * 1e3 / steps
+        f_peak_gb = torch.cuda.max_memory_allocated() / 2 ** 30
 
     # backward only: forward, sync, then time backward (benchmark_backward_speed.py:761-783)
     total = 0.0
     for i in range(warmup + steps):
+        if i == warmup:
+            torch.cuda.reset_peak_memory_stats()
         qg.grad = kg.grad = vg.grad = None
         o = fa.flash_swda_with_sink(qg, kg, vg, W, S)
         torch.cuda.synchronize()
@@ -261,8 +265,60 @@ def time_steps(fa, cfg, q, k, v, do, steps, warmup):
         if i >= warmup:
             total += time.perf_counter() - t0
     b_ms = total * 1e3 / steps
+    b_peak_gb = torch.cuda.max_memory_allocated() / 2 ** 30
     return dict(fwdbwd_ms=fb_ms, fwdbwd_event_ms=fb_event_ms, fwdbwd_median_ms=fb_median_ms, fwd_ms=f_ms,
-                bwd_ms=b_ms, peak_mem_gb=peak_gb)
+                bwd_ms=b_ms, peak_mem_gb=peak_gb, fwd_peak_mem_gb=f_peak_gb, bwd_peak_mem_gb=b_peak_gb)
+
+
+def mode_figures(wl, t):
+    """fwd, bwd and fwd+bwd of one time_steps result: ms, useful TFLOP/s, the fraction of that
+    mode's roofline (max of its useful FLOPs at the MFMA peak and its algorithmic bytes at the HBM
+    peak) and peak memory, as the reference reports them (benchmark_backward_speed.py:720-783)."""
+    out = {}
+    for mode, ms, peak in (("fwd", t["fwd_ms"], t["fwd_peak_mem_gb"]), ("bwd", t["bwd_ms"], t["bwd_peak_mem_gb"]),
+                           ("fwdbwd", t["fwdbwd_ms"], t["peak_mem_gb"])):
+        out[mode] = {"ms": round(ms, 4), "tflops": round(wl.flops(mode) / (ms * 1e-3) / 1e12, 2),
+                     "roofline_us": round(wl.roofline_seconds(mode) * 1e6, 2),
+                     "roofline_frac": round(wl.roofline_seconds(mode) / (ms * 1e-3), 4),
+                     "peak_mem_gb": round(peak, 4)}
+    return out
+
+
+# The reference's own default cases (parse_cases, benchmark_backward_speed.py:829-835): B=1, Hq=16,
+# Hkv in {16, 8, 1}, L=4096, D=16, W=256, S=4; the first is c1, the shape of its published numbers.
+REFERENCE_CASES = {"hkv16": 16, "hkv8": 8, "hkv1": 1}
+
+
+def reference_cases_measure(fa, dev, steps, warmup):
+    """fwd, fwd+bwd and bwd-only times and peak memory of the reference's three default cases in
+    fp16, with mode_figures' roofline fractions."""
+    out = {}
+    for name, hkv in REFERENCE_CASES.items():
+        c = dict(CONFIGS["c1"], Hkv=hkv)
+        qq, kk, vv, dd = make_inputs(c, dev)
+        tt = time_steps(fa, c, qq, kk, vv, dd, steps, warmup)
+        w = _mod("flops").Workload(c["B"], c["Hq"], c["Hkv"], c["L"], c["D"], c["W"], c["S"])
+        out[name] = {"shape": f"B=1 Hq=16 Hkv={hkv} L=4096 D=16 W=256 S=4 fp16", **mode_figures(w, tt)}
+        del qq, kk, vv, dd
+    return out
+
+
+def fp32_measure(fa, cfg, dev, steps, warmup):
+    """The float32 path (q, k, v, o, dq, dk, dv in fp32 on the fp32 matrix instruction) on the
+    config's shape: the three modes, with its useful TFLOP/s against the fp32 MFMA peak."""
+    import torch
+
+    q, k, v, do = (t.float() for t in make_inputs(cfg, dev))
+    tt = time_steps(fa, cfg, q, k, v, do, steps, warmup)
+    w = _mod("flops").Workload(cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"], cfg["D"], cfg["W"], cfg["S"], elem_bytes=4)
+    figs = mode_figures(w, tt)
+    for mode in figs:  # the fp32 roofline: 157.3 TFLOP/s dense fp32 MFMA, 8 TB/s
+        rs = max(w.flops(mode) / 157.3e12, w.bytes(mode) / 8.0e12)
+        figs[mode]["roofline_us"] = round(rs * 1e6, 2)
+        figs[mode]["roofline_frac"] = round(rs / (figs[mode]["ms"] * 1e-3), 4)
+    del q, k, v, do
+    torch.cuda.empty_cache()
+    return {"dtype": "fp32", "peak_tflops": 157.3, **figs}
 
 
 def graph_step_measure(fa, cfg, q, k, v, do, steps):
@@ -709,6 +765,7 @@ def main():
         "fwdbwd_median_ms": round(t["fwdbwd_median_ms"], 4),
         "peak_mem_gb": round(t["peak_mem_gb"], 4),
         "fwdbwd_roofline_frac": round(wl.roofline_seconds("fwdbwd") / (t["fwdbwd_ms"] * 1e-3), 4),
+        "modes": mode_figures(wl, t),
         "clock_warm_steps": warm_steps,
         "kernels": kernels,
         "roofline": roofline,
@@ -728,6 +785,10 @@ def main():
         t1 = time_steps(fa, c1, q1, k1, v1, do1, args.steps, args.warmup)
         line["c1_step"] = {"workload": "c1: " + c1["name"] + ", fwd+bwd", "eager_ms_per_step": round(t1["fwdbwd_ms"], 4),
                            "graph": graph_step_measure(fa, c1, q1, k1, v1, do1, args.steps)}
+        del q1, k1, v1, do1
+        # the reference's default cases, timed by its protocol (its published numbers are c1's)
+        line["reference_cases"] = reference_cases_measure(fa, dev, args.steps, args.warmup)
+        line["fp32_path"] = fp32_measure(fa, cfg, dev, 20, 5)
     if not args.no_sdpa_baseline:
         line["sdpa_baseline"] = sdpa_baseline(cfg, q, k, v, do)
     if not args.no_cpu_baseline:

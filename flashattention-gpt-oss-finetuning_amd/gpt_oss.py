@@ -29,21 +29,24 @@ class _BatchFacts:
     where the packed sequences start, the longest one).  Working them out reads device memory,
     i.e. synchronises the host once; transformers hands the same tensor object to every attention
     layer of a forward pass, so the facts are kept for that tensor (while it lives and is not
-    modified in place) and the other layers enqueue their kernels without waiting for the GPU."""
+    modified in place) and the other layers enqueue their kernels without waiting for the GPU.
 
-    __slots__ = ("_ref", "_key", "_val")
+    The entry is one tuple, replaced by a single store and read once per call, so threads that
+    share the cache (replicas running layers at once) never pair one tensor's facts with
+    another's key."""
+
+    __slots__ = ("_entry",)
 
     def __init__(self):
-        self._ref = None
-        self._key = None
-        self._val = None
+        self._entry = None  # (weakref to the tensor, key, facts)
 
     def get(self, t: torch.Tensor, compute):
         key = (t.data_ptr(), t._version, tuple(t.shape), t.dtype, t.device)
-        if self._ref is not None and self._ref() is t and self._key == key:
-            return self._val
+        entry = self._entry
+        if entry is not None and entry[0]() is t and entry[1] == key:
+            return entry[2]
         val = compute(t)
-        self._ref, self._key, self._val = weakref.ref(t), key, val
+        self._entry = (weakref.ref(t), key, val)
         return val
 
 

@@ -148,8 +148,12 @@ int fa_bwd_dkdv(const fa_bwd_params* p, void* workspace, size_t workspace_bytes,
  * HIP graph capture, tight serving or training loops, harnesses that forbid hipMalloc).  No
  * counterpart in the reference (its backward allocates fp32 staging tensors,
  * flash_attention_gpt_oss.py:397-400).  The workspace is the library's own static device buffer
- * of FA_SCRATCH_BYTES bytes, one per GPU, held from the library's first use on that GPU until the
- * process ends; the call itself allocates and frees nothing.  Same arguments, checks, kernels and
+ * of FA_SCRATCH_BYTES bytes, one per GPU.  The buffer is part of the library's code object, so it is
+ * reserved on a GPU when that object loads there (at the first launch of any of the library's
+ * kernels on it, forward-only use included, whether or not fa_bwd_scratch is ever called) and held
+ * until the process ends; the call itself allocates and frees nothing.  Its first call on a GPU looks
+ * up the buffer's address there (hipGetSymbolAddress): make that call outside any graph capture,
+ * after which calls may be captured.  Same arguments, checks, kernels and
  * results as fa_bwd (bitwise).  Returns FA_ERR_SCRATCH when fa_bwd_workspace_bytes() of the
  * problem exceeds FA_SCRATCH_BYTES.  Every call on one GPU shares that GPU's buffer: calls that
  * overlap in time on one GPU (concurrent streams, or host threads launching without ordering)

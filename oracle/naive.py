@@ -120,6 +120,105 @@ def _fwd_bwd(q, k, v, do, window_size, sink_size, scale, compute_dtype, row_chun
     return o, lse, dq, dk, dv, dsinks
 
 
+@torch.no_grad()
+def sink_key_grads(q, k, v, do, window_size: int, sink_size: int, scale: Optional[float] = None, sinks=None,
+                   compute_dtype=torch.float32, row_chunk: int = 2048):
+    """The gradients that sum over every row of a sequence -- dK/dV of the positional sink keys
+    [0, S) and, with learned `sinks`, dsinks -- for one long sequence ([1, H, L, D] tensors),
+    without the L x L scores.  Rows are taken `row_chunk` at a time; each chunk [r0, r1) runs
+    attention_fwd_bwd(_sinks) on the sub-problem of the sink positions and [r0 - W + 1, r1) (the
+    whole prefix [0, r1) while the chunk's windows reach the sinks), in which every row of the
+    chunk sees exactly its keys of the whole sequence, with dO set to zero on the sub-problem's
+    other rows.  Every row's contribution to these gradients is linear in its dO row, so the
+    zeroed rows add nothing and the chunk sums are exact.  Returns (dk [1, Hkv, S, D],
+    dv [1, Hkv, S, D], dsinks [Hq] or None, sum over rows of |P_sink * delta| [Hq] or None: the
+    size of dsinks' terms), accumulated in float64."""
+    _, Hq, L, D = q.shape
+    Hkv = k.shape[1]
+    S = min(sink_size, L)
+    dk = torch.zeros((1, Hkv, S, D), dtype=torch.float64, device=q.device)
+    dv = torch.zeros_like(dk)
+    ds = None if sinks is None else torch.zeros(Hq, dtype=torch.float64, device=q.device)
+    ds_terms = None if sinks is None else torch.zeros(Hq, dtype=torch.float64, device=q.device)
+    for r0 in range(0, L, row_chunk):
+        r1 = min(L, r0 + row_chunk)
+        t0 = r0 - window_size + 1
+        if t0 <= S:
+            idx = torch.arange(r1, device=q.device)
+        else:
+            idx = torch.cat([torch.arange(S, device=q.device), torch.arange(t0, r1, device=q.device)])
+        sub = lambda t: t.index_select(2, idx)
+        keep = ((idx >= r0) & (idx < r1)).view(1, 1, -1, 1)
+        dos = torch.where(keep, sub(do), torch.zeros((), dtype=do.dtype, device=do.device))
+        if sinks is None:
+            r = attention_fwd_bwd(sub(q), sub(k), sub(v), dos, window_size, sink_size, scale, compute_dtype)
+        else:
+            r = attention_fwd_bwd_sinks(sub(q), sub(k), sub(v), sinks, dos, window_size, sink_size, scale,
+                                        compute_dtype)
+            ds += r[5].double()
+            rows = keep.view(-1)
+            delta = (dos[0][:, rows].to(compute_dtype) * r[0][0][:, rows]).sum(-1)
+            p_sink = torch.exp(sinks.to(compute_dtype).view(-1, 1) - r[1][0][:, rows])
+            ds_terms += (p_sink * delta).abs().sum(-1).double()
+        dk += r[3][:, :, :S].double()
+        dv += r[4][:, :, :S].double()
+    return dk, dv, ds, ds_terms
+
+
+@torch.no_grad()
+def naive_lowp_sink_key_grads(q, k, v, do, window_size: int, sink_size: int, scale: Optional[float] = None,
+                              row_chunk: int = 2048):
+    """dK/dV of the positional sink keys [0, S) as the reference's naive path computes them in the
+    inputs' 16-bit dtype (naive_attention plus autograd; benchmark_backward_speed.py:68-85), for
+    one long sequence ([1, H, L, D] tensors), banded as sink_key_grads is.  The naive path's
+    rounding points are kept: scores = dt(dt(q k^T) * scale), P = softmax in float32 rounded to dt,
+    grad P = dt(dO V^T), grad scores = dt(float32 softmax backward), times scale in dt; each head's
+    dk = dt(grad_scores^T q) and dv = dt(P^T dO) over all of the sequence's rows, then the sum over
+    the KV group's heads rounded to dt once.  Products run in float32 on the 16-bit values (exact
+    products, float32 sums, as the 16-bit GEMMs accumulate), so no 16-bit batched product runs on
+    the GPU.  Returns (dk, dv) [1, Hkv, S, D] as float32 holding dt values."""
+    dt = q.dtype
+    rnd = lambda x: x.to(dt).float()
+    _, Hq, L, D = q.shape
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    S = min(sink_size, L)
+    acc_k = torch.zeros((Hq, S, D), dtype=torch.float32, device=q.device)
+    acc_v = torch.zeros_like(acc_k)
+    for r0 in range(0, L, row_chunk):
+        r1 = min(L, r0 + row_chunk)
+        t0 = r0 - window_size + 1
+        if t0 <= S:
+            idx = torch.arange(r1, device=q.device)
+        else:
+            idx = torch.cat([torch.arange(S, device=q.device), torch.arange(t0, r1, device=q.device)])
+        n = idx.numel()
+        sub = lambda t: t[0].index_select(1, idx).float()
+        qs, ks, vs, dos = sub(q), sub(k), sub(v), sub(do)
+        dos = torch.where(((idx >= r0) & (idx < r1)).view(1, -1, 1), dos, torch.zeros((), device=q.device))
+        kr, vr = ks.repeat_interleave(G, dim=0), vs.repeat_interleave(G, dim=0)
+        sc = rnd(rnd(torch.matmul(qs, kr.transpose(-1, -2).contiguous())) * scale)
+        sc = sc.masked_fill(~allowed_mask(n, window_size, sink_size, device=q.device) if t0 <= S else
+                            ~_sub_allowed(idx, window_size, sink_size), float("-inf"))
+        p32 = torch.softmax(sc, dim=-1)
+        pb = rnd(p32)
+        gp = rnd(torch.matmul(dos, vr.transpose(-1, -2).contiguous()))
+        gs = rnd(rnd(p32 * (gp - (gp * p32).sum(-1, keepdim=True))) * scale)
+        acc_k += torch.matmul(gs[:, :, :S].transpose(-1, -2).contiguous(), qs)
+        acc_v += torch.matmul(pb[:, :, :S].transpose(-1, -2).contiguous(), dos)
+    dk = rnd(rnd(acc_k).view(Hkv, G, S, D).sum(1)).unsqueeze(0)
+    dv = rnd(rnd(acc_v).view(Hkv, G, S, D).sum(1)).unsqueeze(0)
+    return dk, dv
+
+
+def _sub_allowed(idx, window_size, sink_size):
+    """allowed_mask over the true positions `idx` of a sub-problem (rows and keys alike)."""
+    qq, kk = idx.view(-1, 1), idx.view(1, -1)
+    return (kk <= qq) & (((qq - kk) < window_size) | (kk < sink_size))
+
+
 def gpt_oss_eager(q, k, v, sinks, window_size: Optional[int], scale: float):
     """The eager GPT-OSS attention of HF transformers (modeling_gpt_oss.py eager_attention_forward),
     restated on [B, H, L, D] tensors in their own dtype: repeated K/V, scaled scores plus the

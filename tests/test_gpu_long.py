@@ -14,6 +14,16 @@ stay the first S keys, so the sampled rows see exactly the keys they see in the 
 (every key they can reach lies at or past r0 - W + 1 > t0).  Their O, LSE and dQ must therefore
 agree; at the end of a sequence (r0 = L - 64) every row that reaches the last 64 keys is sampled,
 so those keys' dK and dV must agree too.  Every head is checked, at test_gpu_parity.py's bar.
+
+The gradients that sum over every row of a sequence -- dK/dV of the positional sink keys, which
+every row sees, and the learned sinks' gradient -- are checked over every row of every sequence:
+naive.sink_key_grads runs the oracle over 2048-row chunks, each on a sub-problem in which the
+chunk's rows see exactly their keys and the other rows' dO is zero.  dK/dV rows of sink keys sum
+G x L (about a million) rounded terms each, so they get test_gpu_parity.py's bar for sink-key rows:
+a = max(2e-2, 2 x the error of the reference's naive 16-bit path), that path's sink-key gradients
+computed banded in the same way with its rounding points kept (naive.naive_lowp_sink_key_grads,
+pinned against naive_attention's autograd backward on the CPU).  dsinks has test_gpu_sinks.py's
+bound, 2e-2 (1 + sum |P_sink delta|).
 """
 import math
 
@@ -34,6 +44,26 @@ def subproblem_keys(r0, W, S):
     t0 = r0 - W - 64
     assert t0 >= S
     return torch.cat([torch.arange(S), torch.arange(t0, r0 + 64)])
+
+
+def check_sink_key_grads(tag, q, k, v, do, dk, dv, W, S, scale, sinks=None):
+    """dK/dV rows [0, S) of one sequence ([1, H, L, D] views; dk, dv the kernel's [1, Hkv, S, D] rows)
+    against naive.sink_key_grads over all of its rows; returns that function's (dsinks, terms)."""
+    rdk, rdv, rds, terms = naive.sink_key_grads(q, k, v, do, W, S, scale, sinks=sinks, row_chunk=2048)
+    if S > 0:
+        ndk, ndv = naive.naive_lowp_sink_key_grads(q, k, v, do, W, S, scale, row_chunk=2048)
+        every = torch.ones((1, 1, 1, 1), dtype=torch.bool)
+        assert_close(f"dK sink keys {tag}", dk, rdk, ndk, every)
+        assert_close(f"dV sink keys {tag}", dv, rdv, ndv, every)
+    return rds, terms
+
+
+def check_dsinks_sum(got, ref, terms):
+    """dsinks summed over every row of every sequence, at 2e-2 (1 + sum |P_sink delta|) per head."""
+    err = (got.double() - ref).abs()
+    bound = 2e-2 * (1.0 + terms)
+    print(f"  dsinks: max abs err {float(err.max()):.3e}, largest err / bound {float((err / bound).max()):.3f}")
+    assert bool((err <= bound).all()), f"dsinks: err {err.tolist()} bound {bound.tolist()}"
 
 
 def _randn(B, H, seed, layout):
@@ -64,12 +94,25 @@ def test_long_context_past_4gb(gpu, W, S, layout, learned):
     sk = (2.0 * torch.randn(HQ, generator=torch.Generator().manual_seed(5))).to(torch.bfloat16).float().cuda() \
         if learned else None
     o, lse = ops.forward(q, k, v, W, S, sc, sinks=sk)
-    dq, dk, dv = ops.backward(q, k, v, o, lse, do, W, S, sc, sinks=sk)[:3]
+    grads = ops.backward(q, k, v, o, lse, do, W, S, sc, sinks=sk)
+    dq, dk, dv = grads[:3]
     torch.cuda.synchronize()
+    # the sums over every row: sink keys' dK/dV of every sequence, and dsinks over all of them
+    ds_ref = torch.zeros(HQ, dtype=torch.float64, device="cuda")
+    ds_terms = torch.zeros_like(ds_ref)
+    for b in range(B):
+        one = lambda t: t[b:b + 1]
+        rds, terms = check_sink_key_grads(f"b={b}", one(q), one(k), one(v), one(do), dk[b:b + 1, :, :S],
+                                          dv[b:b + 1, :, :S], W, S, sc, sinks=sk)
+        if learned:
+            ds_ref += rds
+            ds_terms += terms
+    if learned:
+        check_dsinks_sum(grads[3], ds_ref, ds_terms)
     for b, r0 in ((B - 1, L - 64), (B - 1, L // 2 + 13), (3, 100000), (0, 4096)):
         idx = subproblem_keys(r0, W, S).cuda()
         sub = lambda t: t[b:b + 1].index_select(2, idx).contiguous()
-        if learned:  # the sink gradient sums every row of a head: not checked on samples
+        if learned:
             ro, rlse, rdq, rdk, rdv, _ = naive.attention_fwd_bwd_sinks(sub(q), sub(k), sub(v), sk, sub(do), W, S,
                                                                        scale=sc, compute_dtype=torch.float32)
         else:
@@ -84,7 +127,7 @@ def test_long_context_past_4gb(gpu, W, S, layout, learned):
         if r0 + 64 == L:
             assert_close(f"dK {tag}", dk[b, :, rows], rdk[0, :, n - 64:])
             assert_close(f"dV {tag}", dv[b, :, rows], rdv[0, :, n - 64:])
-    del q, k, v, do, o, lse, dq, dk, dv
+    del q, k, v, do, o, lse, dq, dk, dv, grads
     torch.cuda.empty_cache()
 
 
@@ -106,6 +149,12 @@ def test_long_packed_batch(gpu):
     o, lse = ops.forward_varlen(q, k, v, cu_dev, max_len, W, S, sc)
     dq, dk, dv = ops.backward_varlen(q, k, v, o, lse, do, cu_dev, max_len, W, S, sc)
     torch.cuda.synchronize()
+    # the sink keys' dK/dV of each sequence, over all of its rows
+    for s, (lo, hi) in enumerate(zip(cu[:-1], cu[1:])):
+        as4 = lambda t: t[lo:hi].permute(1, 0, 2).unsqueeze(0)
+        n_s = min(S, hi - lo)
+        check_sink_key_grads(f"sequence {s}", as4(q), as4(k), as4(v), as4(do), as4(dk)[:, :, :n_s],
+                             as4(dv)[:, :, :n_s], W, S, sc)
     # (sequence, first sampled row relative to its start; None: the whole sequence)
     for s, r0 in ((0, 131072 - 64), (0, 70001), (1, None), (2, 8927 - 64), (3, 33333)):
         lo, n_seq = cu[s], cu[s + 1] - cu[s]

@@ -3,13 +3,16 @@ inputs.
 
 Tolerance, elementwise on O, LSE, dQ, dK and dV:
     |ours - ref| <= a + 2e-2 * |ref|,   a = 2e-2
-(the north-star bar for 16-bit outputs).  For the small cases the reference's own naive path
-(scores in the input dtype, fp32 softmax, autograd backward; benchmark_backward_speed.py:68-85)
-is also run, on the CPU, on the same inputs, and a = max(2e-2, 2 * its max-abs error): dK/dV
-rows of sink keys sum hundreds of large terms, and there rounding dS/P to 16 bits (which the
-reference's kernels do as well, benchmark_backward_speed.py:284-286) legitimately exceeds
-2e-2 -- the reference path itself does (the FlashAttention test convention: no worse than
-twice the low-precision reference).  The full-size configs use a = 2e-2.
+(the north-star bar for 16-bit outputs), on every element with one exception: the dK/dV rows of
+the sink keys (k < S).  A sink key is seen by every row of its sequence, so its dK/dV row adds
+G x L rounded terms, and rounding P and dS to 16 bits (which the reference's kernels do as well,
+benchmark_backward_speed.py:284-286) legitimately moves such a sum by more than 2e-2 -- the
+reference's own naive path (scores in the input dtype, fp32 softmax, autograd backward;
+benchmark_backward_speed.py:68-85) does.  For those rows only, when a case also runs that naive
+path (on the CPU, same inputs), a = max(2e-2, 2 x the naive path's largest error over those same
+rows) (the FlashAttention test convention: no worse than twice the low-precision reference).
+Every other element, the sink-key rows of cases without the naive path and every full-size
+config keep a = 2e-2.
 
 Inputs follow the reference protocol: a seeded CPU generator draws q, k, v, then dO from
 N(0, 1) in float32, cast to the case dtype and copied to the GPU, so the oracle (evaluated in
@@ -38,20 +41,38 @@ def make_inputs(B, Hq, Hkv, L, D, dtype, seed, do_std=1.0, device="cuda"):
     return [t.to(dtype).to(device) for t in (q, k, v, do)]
 
 
-def assert_close(name, got, ref, naive=None):
+def assert_close(name, got, ref, naive=None, wide_rows=None):
+    """|got - ref| <= a + RTOL |ref| elementwise, a = ATOL.  With `naive` (the low-precision naive
+    path's result) and `wide_rows` (a boolean mask broadcastable to the tensor that marks the dK/dV
+    rows of sink keys), a on those elements only is max(ATOL, 2 x the naive path's largest error
+    over them)."""
     got = got.float()
     ref = ref.float()
     assert torch.isfinite(got).all(), f"{name}: non-finite values"
     err = (got - ref).abs()
-    a = ATOL
-    if naive is not None:
-        a = max(ATOL, 2.0 * float((naive.float().to(ref.device) - ref).abs().max()))
-    bad = err > (a + RTOL * ref.abs())
+    a = torch.full_like(ref, ATOL)
+    a_wide = ATOL
+    if naive is not None and wide_rows is not None:
+        wide = torch.broadcast_to(wide_rows.to(ref.device), ref.shape)
+        if wide.any():
+            nerr = (naive.float().to(ref.device) - ref).abs()
+            a_wide = max(ATOL, 2.0 * float(nerr[wide].max()))
+            a = torch.where(wide, torch.full_like(ref, a_wide), a)
+    need = err - RTOL * ref.abs()  # the smallest a that each element passes with
+    plain = need if a_wide == ATOL else need[a == ATOL]
+    print(f"  {name}: max abs err {float(err.max()):.3e}, need_a {float(plain.max()) if plain.numel() else 0.0:.3e}"
+          + (f", sink-key rows a {a_wide:.3e}" if a_wide > ATOL else ""))
+    bad = need > a
     if bad.any():
         idx = tuple(int(i) for i in bad.nonzero()[0])
-        raise AssertionError(f"{name}: {int(bad.sum())} elements out of tolerance (a={a:.3g}); max abs err "
-                             f"{float(err.max()):.4g}; first at {idx}: got {float(got[idx]):.6g} ref "
-                             f"{float(ref[idx]):.6g}")
+        raise AssertionError(f"{name}: {int(bad.sum())} elements out of tolerance (a={ATOL:.3g}, sink-key rows "
+                             f"{a_wide:.3g}); max abs err {float(err.max()):.4g}; first at {idx}: got "
+                             f"{float(got[idx]):.6g} ref {float(ref[idx]):.6g} a {float(a[idx]):.3g}")
+
+
+def sink_rows(L, S, device="cuda"):
+    """[1, 1, L, 1] mask of the sink keys' rows of a [B, H, L, D] dK/dV tensor."""
+    return (torch.arange(L, device=device) < S).view(1, 1, L, 1)
 
 
 def naive_reference(q, k, v, do, W, S, scale):
@@ -76,17 +97,17 @@ def run_case(B, Hq, Hkv, L, D, W, S, dtype, seed=0, scale=None, heads=None, do_s
                                                       row_chunk=2048, heads=heads)
     if with_naive is None:
         with_naive = heads is None and B * Hq * L * L <= (1 << 26)
-    nv = naive_reference(q, k, v, do, W, S, sc) if with_naive else (None,) * 4
+    nv = naive_reference(q, k, v, do, W, S, sc) if with_naive and S > 0 else (None,) * 4
     G = Hq // Hkv
     hs = list(range(Hq)) if heads is None else list(heads)
     sel = lambda t, idx: None if t is None else t[:, idx]
-    assert_close("O", o[:, hs], ro[:, hs], sel(nv[0], hs))
+    assert_close("O", o[:, hs], ro[:, hs])
     assert_close("LSE", lse[:, hs], rlse[:, hs])
-    assert_close("dQ", dq[:, hs], rdq[:, hs], sel(nv[1], hs))
+    assert_close("dQ", dq[:, hs], rdq[:, hs])
     groups = [g for g in range(Hkv) if all(h in hs for h in range(g * G, (g + 1) * G))]
     assert groups, "choose heads covering at least one KV group"
-    assert_close("dK", dk[:, groups], rdk[:, groups], sel(nv[2], groups))
-    assert_close("dV", dv[:, groups], rdv[:, groups], sel(nv[3], groups))
+    assert_close("dK", dk[:, groups], rdk[:, groups], sel(nv[2], groups), sink_rows(L, S))
+    assert_close("dV", dv[:, groups], rdv[:, groups], sel(nv[3], groups), sink_rows(L, S))
     return o, lse, dq, dk, dv
 
 

@@ -2,9 +2,10 @@
 [B, L, H, D] layout, and transformers' GptOssAttention running on the gfx950 kernels.
 
 O, LSE, dQ, dK, dV use the tolerance of test_gpu_parity.py, with the oracle
-naive.attention_fwd_bwd_sinks in float32 and, for the small cases, the low-precision naive path
-naive.gpt_oss_eager (transformers' eager GPT-OSS attention restated, in the input dtype, on
-the CPU) setting a = max(2e-2, 2 * its error).  The sink gradient of head h is a sum over every
+naive.attention_fwd_bwd_sinks in float32: a = 2e-2 everywhere except the dK/dV rows of positional
+sink keys (k < S), where for the small cases the low-precision naive path (transformers' eager
+GPT-OSS attention restated, in the input dtype, on the CPU) sets a = max(2e-2, 2 * its error over
+those rows).  The sink gradient of head h is a sum over every
 row of the head, dsink = -sum P_sink * delta, so its bound scales with the size of that sum:
     |ours - ref| <= 2e-2 * (1 + sum over rows of |P_sink * delta|)
 (or twice the naive path's error, if larger).
@@ -16,7 +17,7 @@ import torch
 
 from conftest import load_mod, load_pkg
 from oracle import naive
-from test_gpu_parity import BF, FP, assert_close, make_inputs
+from test_gpu_parity import BF, FP, assert_close, make_inputs, sink_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -76,12 +77,12 @@ def run_sinks_case(B, Hq, Hkv, L, D, W, S, dtype, seed=0, sink_scale=2.0, sinks=
     G = Hq // Hkv
     hs = list(range(Hq)) if heads is None else list(heads)
     sel = lambda t, idx: None if t is None else t[:, idx]
-    assert_close("O", o[:, hs], ro[:, hs], sel(nv[0], hs))
+    assert_close("O", o[:, hs], ro[:, hs])
     assert_close("LSE", lse[:, hs], rlse[:, hs])
-    assert_close("dQ", dq[:, hs], rdq[:, hs], sel(nv[1], hs))
+    assert_close("dQ", dq[:, hs], rdq[:, hs])
     groups = [g for g in range(Hkv) if all(h in hs for h in range(g * G, (g + 1) * G))]
-    assert_close("dK", dk[:, groups], rdk[:, groups], sel(nv[2], groups))
-    assert_close("dV", dv[:, groups], rdv[:, groups], sel(nv[3], groups))
+    assert_close("dK", dk[:, groups], rdk[:, groups], sel(nv[2], groups), sink_rows(L, S))
+    assert_close("dV", dv[:, groups], rdv[:, groups], sel(nv[3], groups), sink_rows(L, S))
     check_dsinks(ds, rds, rlse, ro, do, sinks, hs, nv[4])
     return o, lse, dq, dk, dv, ds
 

@@ -1,9 +1,10 @@
 """GPU parity of variable-length (packed) batches: fa_fwd_varlen / fa_bwd_varlen against the
 float32 variable-length oracle on the same seeded inputs.
 
-Same bar as tests/test_gpu_parity.py: elementwise |ours - ref| <= a + 2e-2 |ref| with
-a = max(2e-2, 2 x the max error of the reference's naive path in the input dtype), the naive
-path being run per sequence on the CPU (with learned sinks, the GPT-OSS eager path of
+Same bar as tests/test_gpu_parity.py: elementwise |ours - ref| <= a + 2e-2 |ref| with a = 2e-2,
+except on the dK/dV rows of each sequence's positional sink keys, where
+a = max(2e-2, 2 x the max error over those rows of the reference's naive path in the input dtype),
+the naive path being run per sequence on the CPU (with learned sinks, the GPT-OSS eager path of
 tests/test_gpu_sinks.py).  The sink gradient uses that file's bound, which scales with the sum
 over rows of |P_sink * delta|.  Cases mix long, short, length-1 and empty sequences,
 both sink paths (S <= 16 in the dQ kernel, S > 16 in chunk workgroups), learned sinks, full
@@ -68,12 +69,18 @@ def run_varlen(cu, Hq, Hkv, D, W, S, dtype, seed=0, sinks=False, with_naive=True
     torch.cuda.synchronize()
     ref = naive.attention_fwd_bwd_varlen(q, k, v, do, torch.tensor(cu), Wk, S, scale, sinks=sk,
                                          compute_dtype=torch.float32, row_chunk=1024)
-    nv = naive_packed(q, k, v, do, cu, Wk, S, scale, sinks=sk) if with_naive else (None,) * 5
-    assert_close("O", o, ref[0], nv[0])
+    nv = naive_packed(q, k, v, do, cu, Wk, S, scale, sinks=sk) if with_naive and (S > 0 or sinks) else (None,) * 5
+    # rows [cu[b], cu[b] + S) of each sequence hold its sink keys
+    pos = torch.arange(total)
+    wide = torch.zeros(total, dtype=torch.bool)
+    for lo, hi in zip(cu[:-1], cu[1:]):
+        wide |= (pos >= lo) & (pos < min(hi, lo + S))
+    wide = wide.view(total, 1, 1)
+    assert_close("O", o, ref[0])
     assert_close("LSE", lse, ref[1])
-    assert_close("dQ", grads[0], ref[2], nv[1])
-    assert_close("dK", grads[1], ref[3], nv[2])
-    assert_close("dV", grads[2], ref[4], nv[3])
+    assert_close("dQ", grads[0], ref[2])
+    assert_close("dK", grads[1], ref[3], nv[2], wide)
+    assert_close("dV", grads[2], ref[4], nv[3], wide)
     if sinks:
         as_b1 = lambda t: t.permute(1, 0, 2).unsqueeze(0)
         check_dsinks(grads[3], ref[5], ref[1].unsqueeze(0), as_b1(ref[0]), as_b1(do), sk, range(Hq), nv[4])

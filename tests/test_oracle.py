@@ -205,3 +205,67 @@ def test_long_context_subproblem_is_exact(L, W, S, r0, learned):
             torch.testing.assert_close(sub[i][:, :, n - 64:], full[i][:, :, rows])
     else:  # away from the end, the keys also get gradient from rows past the sample
         assert not torch.allclose(sub[3][:, :, n - 64:], full[3][:, :, rows])
+
+
+@pytest.mark.parametrize("L,W,S,chunk,learned", [(900, 128, 4, 100, False), (1000, 300, 40, 256, False),
+                                                 (700, 1, 3, 64, False), (500, 2000, 5, 128, False),
+                                                 (900, 128, 0, 128, True), (800, 64, 6, 97, True)])
+def test_sink_key_grads_equal_the_whole_sequence(L, W, S, chunk, learned):
+    """naive.sink_key_grads (row chunks on sub-problems, dO zeroed outside the chunk) gives the sink
+    keys' dK/dV rows and the learned sinks' gradient of the whole-sequence oracle, in float64;
+    keeping the sub-problems' other rows instead of zeroing their dO does not."""
+    q, k, v, do = _inputs(1, 4, 2, L, 8, seed=L + W)
+    sk = torch.randn(4, dtype=torch.float64, generator=torch.Generator().manual_seed(W)) if learned else None
+    if learned:
+        full = naive.attention_fwd_bwd_sinks(q, k, v, sk, do, W, S, compute_dtype=torch.float64)
+    else:
+        full = naive.attention_fwd_bwd(q, k, v, do, W, S, compute_dtype=torch.float64)
+    dk, dv, ds, ds_terms = naive.sink_key_grads(q, k, v, do, W, S, sinks=sk, compute_dtype=torch.float64,
+                                                row_chunk=chunk)
+    torch.testing.assert_close(dk, full[3][:, :, :S])
+    torch.testing.assert_close(dv, full[4][:, :, :S])
+    if learned:
+        torch.testing.assert_close(ds, full[5])
+        delta = (do * full[0]).sum(-1)
+        terms = (torch.exp(sk.view(1, -1, 1) - full[1]) * delta).abs().sum(dim=(0, 2))
+        torch.testing.assert_close(ds_terms, terms)
+    else:
+        assert ds is None and ds_terms is None
+    # without the zeroing, the rows before each chunk (whose windows the sub-problem truncates) count
+    # again: a mistake this check is there to catch
+    if S > 0 and L > chunk + W:
+        wrong = torch.zeros_like(dk)
+        for r0 in range(0, L, chunk):
+            r1 = min(L, r0 + chunk)
+            t0 = r0 - W + 1
+            idx = torch.arange(r1) if t0 <= S else torch.cat([torch.arange(S), torch.arange(t0, r1)])
+            r = naive.attention_fwd_bwd(*(t.index_select(2, idx) for t in (q, k, v, do)), W, S,
+                                        compute_dtype=torch.float64)
+            wrong += r[3][:, :, :S]
+        assert not torch.allclose(wrong, full[3][:, :, :S])
+
+
+@pytest.mark.parametrize("L,W,S,chunk,dt", [(1500, 128, 4, 256, torch.bfloat16), (1200, 300, 40, 200, torch.float16),
+                                            (800, 50, 3, 100, torch.bfloat16), (300, 1000, 6, 64, torch.float16)])
+def test_lowp_sink_key_grads_follow_the_naive_path(L, W, S, chunk, dt):
+    """naive.naive_lowp_sink_key_grads (the naive 16-bit path's rounding points, banded, float32
+    products) gives the sink keys' dK/dV of naive_attention's own autograd backward in that dtype:
+    at least 99% of the values bit for bit, the rest within one unit in the last place at the
+    tensor's largest magnitude (a float32 sum taken in another order can round one 16-bit value
+    the other way); so its error against the float64 oracle is the naive path's."""
+    g = torch.Generator().manual_seed(L + S)
+    Hq, Hkv, D = 8, 2, 64
+    q, k, v, do = (torch.randn(1, h, L, D, generator=g).to(dt) for h in (Hq, Hkv, Hkv, Hq))
+    qc, kc, vc = (t.clone().requires_grad_() for t in (q, k, v))
+    naive.naive_attention(qc, kc, vc, W, S).backward(do)
+    dk, dv = naive.naive_lowp_sink_key_grads(q, k, v, do, W, S, row_chunk=chunk)
+    ulp = 2.0 ** -7 if dt is torch.bfloat16 else 2.0 ** -10
+    for got, want in ((dk, kc.grad[:, :, :S].float()), (dv, vc.grad[:, :, :S].float())):
+        assert got.dtype == torch.float32 and torch.equal(got, got.to(dt).float())
+        diff = (got - want).abs()
+        assert float(diff.max()) <= ulp * float(want.abs().max()), float(diff.max())
+        assert int((diff > 0).sum()) <= diff.numel() // 100, int((diff > 0).sum())
+    ref = naive.attention_fwd_bwd(q, k, v, do, W, S, compute_dtype=torch.float64)
+    err_naive = float((kc.grad[:, :, :S].double() - ref[3][:, :, :S]).abs().max())
+    err_emul = float((dk.double() - ref[3][:, :, :S]).abs().max())
+    assert abs(err_emul - err_naive) <= 0.1 * err_naive
