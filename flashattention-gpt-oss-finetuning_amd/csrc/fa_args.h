@@ -66,6 +66,13 @@ struct Args {
   // tensors of total_rows packed rows (L is then the longest sequence, batch strides are 0)
   const int* cu_seqlens;
   int total_rows;
+  // Packed batches: the sliding kernels' units and the dK/dV kernel's 64-key workgroups are handed
+  // out over the pieces the sequences hold (varlen_nth), so no workgroup is launched for a piece
+  // past a short sequence's end.  vl_units units per (KV head, head group) and vl_kblocks key
+  // blocks per KV head bound those pieces; 0: the fixed-length enumeration (B x slide_ncu units,
+  // B x n_kblocks blocks).
+  int vl_units;
+  int vl_kblocks;
 };
 
 // Sequence b: its length and the row where it starts in the packed tensors (fixed-length
@@ -84,6 +91,46 @@ __device__ __forceinline__ Seq seq_of(const A& a, int b) {
   hi = hi < lo ? lo : (hi > a.total_rows ? a.total_rows : hi);
   const int n = hi - lo;
   return Seq{n < a.L ? n : a.L, lo};
+}
+
+// Packed batches: sequence b holds ceil(ceil(L_b / rows) / per) pieces of `per` blocks of `rows`
+// rows, and `slots` >= their number N of workgroups enumerate them, the sequences' pieces in order
+// after slots - N that have none (so that the empty ones, which exit at once, are dispatched
+// first and every piece gets a place in the first round).  For the wave-uniform slot index p, sets
+// b and the piece's index within its sequence and returns true, or returns false for an empty
+// slot.  Wave-wide prefix sums over the sequences, 64 per round: every lane of the wave must call
+// it.  (The results are made scalar so that the callers' index arithmetic stays scalar.)
+template <typename A>
+__device__ inline bool varlen_nth(const A& a, int p, int slots, int rows, int per, int& b, int& piece) {
+  const int lane = threadIdx.x & 63;
+  auto count = [&](int bb) { return bb < a.B ? ((seq_of(a, bb).L + rows - 1) / rows + per - 1) / per : 0; };
+  auto prefix = [&](int n) {  // inclusive prefix sum over the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(n, o);
+      if (lane >= o) n += y;
+    }
+    return n;
+  };
+  int total = 0;
+  for (int b0 = 0; b0 < a.B; b0 += 64) total += __builtin_amdgcn_readfirstlane(__shfl(prefix(count(b0 + lane)), 63));
+  p -= slots - total;
+  if (p < 0) return false;
+  int base = 0;
+  for (int b0 = 0; b0 < a.B; b0 += 64) {
+    const int n = count(b0 + lane);
+    const int x = prefix(n);
+    const int tot = __builtin_amdgcn_readfirstlane(__shfl(x, 63));
+    if (p < base + tot) {
+      const unsigned long long m = __ballot(base + x > p);
+      const int l = __builtin_amdgcn_readfirstlane(__ffsll(m) - 1);  // the first sequence whose pieces reach past p
+      b = b0 + l;
+      piece = __builtin_amdgcn_readfirstlane(p - base - (__shfl(x, l) - __shfl(n, l)));
+      return true;
+    }
+    base += tot;
+  }
+  return false;
 }
 
 // Element offset of row `row` of (batch b, head h) of a tensor with strides s[3] (a plain array

@@ -622,9 +622,27 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   const int per_group = a.n_kblocks + a.nsp * a.n_chunks;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   // groups in (KV head, batch) order, the KV head outermost: the XCDs then split over KV heads
-  // before sequences, which keeps their work even for sequences of different lengths
-  const int grp = id / per_group, r = id % per_group;
-  const int kvh = grp / a.B, b = grp % a.B;
+  // before sequences, which keeps their work even for sequences of different lengths.  A packed
+  // batch hands out only the key blocks with keys: per KV head, each sequence's blocks
+  // (varlen_nth), then the sequences' chunk workgroups.
+  int kvh, b, r;
+  if (a.vl_kblocks) {
+    const int n_cw = a.nsp * a.n_chunks;
+    const int per_kv = a.vl_kblocks + a.B * n_cw;
+    kvh = id / per_kv;
+    const int p = id % per_kv;
+    if (p < a.vl_kblocks) {
+      if (!varlen_nth(a, p, a.vl_kblocks, kKvKeys, 1, b, r)) return;
+    } else {
+      b = (p - a.vl_kblocks) / n_cw;
+      r = a.n_kblocks + (p - a.vl_kblocks) % n_cw;
+    }
+  } else {
+    const int grp = id / per_group;
+    r = id % per_group;
+    kvh = grp / a.B;
+    b = grp % a.B;
+  }
   const Seq sq = seq_of(a, b);
   const int L = sq.L;
   int kblk, chunk = -1, qlo, qhi;
@@ -1498,14 +1516,14 @@ static hipError_t launch_dkdv_d(const Args& a, hipStream_t stream) {
       e = hipGetLastError();
       folded = dkdv4_folds_in_kernel(ad, D, dkdv4_lds_elems<D>());
     } else {
-      hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), dim3(a.n_chunk_wgs + a.B * a.Hkv * a.n_kblocks), dim3(256), 0,
-                         stream, ad);
+      const int per_kv = a.vl_kblocks ? a.vl_kblocks : a.B * a.n_kblocks;  // regular workgroups per KV head
+      hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), dim3(a.n_chunk_wgs + a.Hkv * per_kv), dim3(256), 0, stream, ad);
       e = hipGetLastError();
       folded = dkdv_folds_in_kernel(ad, D);
     }
   } else {
-    hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), dim3(a.n_chunk_wgs + a.B * a.Hkv * a.n_kblocks), dim3(256), 0, stream,
-                       ad);
+    const int per_kv = a.vl_kblocks ? a.vl_kblocks : a.B * a.n_kblocks;
+    hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), dim3(a.n_chunk_wgs + a.Hkv * per_kv), dim3(256), 0, stream, ad);
     e = hipGetLastError();
     folded = dkdv_folds_in_kernel(ad, D);
   }

@@ -32,7 +32,9 @@ constexpr int kRing = kSlideRing;  // window slots (fa_plan.h); slot kRing holds
 
 }  // namespace
 
-template <typename E, bool SINK>
+// VL: a packed batch's enumeration of the units (a separate instantiation, so that the
+// fixed-length kernel's code and registers are not touched by it).
+template <typename E, bool SINK, bool VL>
 __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
   constexpr int D = 64;
   constexpr int KS = D / 16;
@@ -52,14 +54,27 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
   const int W = a.W, S = a.S;
 
   // unit -> (KV head, batch, head group, chunk), chunks fastest; a contiguous range of units per
-  // XCD, so the chunks of one (batch, KV head) share that XCD's L2
+  // XCD, so the chunks of one (batch, KV head) share that XCD's L2.  A packed batch hands out only
+  // the chunks with rows: (KV head, head group), then each sequence's chunks.  `slot` is the unit's
+  // index in the (KV head, batch, head group, chunk) enumeration either way: its sink-key partials
+  // go to slot `slot`, where the folds look for them.
   const int hg_n = a.G / kSlideWaves;
   const int unit = xcd_remap(blockIdx.x, gridDim.x);
-  const int chunk = unit % a.slide_ncu;
-  const int rest = unit / a.slide_ncu;
-  const int hg = rest % hg_n;
-  const int bk = rest / hg_n;
-  const int b = bk % a.B, kvh = bk / a.B;
+  int chunk, hg, b, kvh;
+  if constexpr (VL) {
+    const int grp = unit / a.vl_units;
+    hg = grp % hg_n;
+    kvh = grp / hg_n;
+    if (!varlen_nth(a, unit % a.vl_units, a.vl_units, 32, a.slide_ct, b, chunk)) return;
+  } else {
+    chunk = unit % a.slide_ncu;
+    const int rest = unit / a.slide_ncu;
+    hg = rest % hg_n;
+    const int bk = rest / hg_n;
+    b = bk % a.B;
+    kvh = bk / a.B;
+  }
+  const int slot = VL ? ((kvh * a.B + b) * hg_n + hg) * a.slide_ncu + chunk : unit;
   const Seq sq = seq_of(a, b);
   const int L = sq.L;
   const int n_qt = (L + 31) / 32;
@@ -391,22 +406,28 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
       }
     __syncthreads();
     const int n_out = 2 * sr * D;
-    float* slot = A.dq_sink_part + int64_t(unit) * n_out;
+    float* dst = A.dq_sink_part + int64_t(slot) * n_out;
     for (int x = tid; x < n_out; x += 512) {
       const int kind = x / (sr * D), rr = x % (sr * D);
       float v = 0.f;
 #pragma unroll
       for (int w = 0; w < kSlideWaves; ++w) v += red[(w * 2 + kind) * sr * D + rr];
-      slot[x] = v;
+      dst[x] = v;
     }
   }
 }
 
 template <typename E>
 static hipError_t launch_slide_e(const Args& a, hipStream_t stream) {
-  const dim3 grid(unsigned(a.B * a.Hkv * (a.G / kSlideWaves) * a.slide_ncu)), block(512);
-  if (a.sink_dq) hipLaunchKernelGGL((bwd_dq_slide_kernel<E, true>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((bwd_dq_slide_kernel<E, false>), grid, block, 0, stream, a);
+  const int per = a.vl_units ? a.vl_units : a.B * a.slide_ncu;  // units per (KV head, head group)
+  const dim3 grid(unsigned(a.Hkv * (a.G / kSlideWaves) * per)), block(512);
+  if (a.vl_units) {
+    if (a.sink_dq) hipLaunchKernelGGL((bwd_dq_slide_kernel<E, true, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((bwd_dq_slide_kernel<E, false, true>), grid, block, 0, stream, a);
+  } else {
+    if (a.sink_dq) hipLaunchKernelGGL((bwd_dq_slide_kernel<E, true, false>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((bwd_dq_slide_kernel<E, false, false>), grid, block, 0, stream, a);
+  }
   return hipGetLastError();
 }
 

@@ -186,6 +186,17 @@ int slide_units_ct(const fa::Args& a, int64_t slots) {
   return int(std::max<int64_t>(ct, 1));
 }
 
+// Packed batches, the sliding kernels: units per (KV head, head group) that the sequences' rows can
+// fill -- sequence b needs ceil(ceil(L_b / 32) / ct) <= L_b / (32 ct) + 1 units, so at most
+// ceil(total_rows / (32 ct)) + B in all -- when fewer than B x slide_ncu (see fa::Args); 0 for a
+// fixed-length batch.
+int vl_units(const fa::Args& a) {
+  if (!a.cu_seqlens) return 0;
+  const int64_t rows_ct = 32 * int64_t(a.slide_ct);
+  const int64_t bound = (int64_t(a.total_rows) + rows_ct - 1) / rows_ct + a.B;
+  return bound < int64_t(a.B) * a.slide_ncu ? int(bound) : 0;
+}
+
 // The sliding dQ kernel (fa_bwd_slide.hip) serves D = 64 16-bit backwards whose KV groups hold a
 // multiple of 8 query heads, with a window of 1..161 keys (at most 6 key halves of 32 in LDS) and
 // at most 32 sink keys (one sink half).  Its workgroups take slide_ct consecutive 32-row tiles,
@@ -199,6 +210,7 @@ void plan_slide(fa::Args& a, int D) {
   a.dq_slide = 1;
   a.slide_ct = int(ct);
   a.slide_ncu = int((n_qt + ct - 1) / ct);
+  a.vl_units = vl_units(a);
 }
 
 // The sliding forward (fa_fwd.hip fwd_slide_kernel): the same shapes with W <= 129; two
@@ -211,7 +223,16 @@ bool plan_fwd_slide(fa::Args& a, int D, int dtype) {
   const int64_t ct = slide_units_ct(a, 2 * int64_t(device_cus()));
   a.slide_ct = int(ct);
   a.slide_ncu = int((n_qt + ct - 1) / ct);
+  a.vl_units = vl_units(a);
   return true;
+}
+
+// Packed batches, the dK/dV kernel: key blocks per KV head that the sequences' keys can fill
+// (each sequence adds at most one partial block), when fewer than B x n_kblocks (see fa::Args).
+int vl_kblocks(const fa::Args& a) {
+  if (!a.cu_seqlens) return 0;
+  const int64_t bound = (int64_t(a.total_rows) + fa::kKvKeys - 1) / fa::kKvKeys + a.B;
+  return bound < int64_t(a.B) * a.n_kblocks ? int(bound) : 0;
 }
 
 fa::Args base_args(int32_t B, int32_t Hq, int32_t Hkv, int32_t L, int32_t D, int32_t W, int32_t S,
@@ -583,6 +604,7 @@ int fa_bwd_varlen(const fa_bwd_params* p, const int32_t* cu_seqlens, int32_t tot
   if ((sinks && !aligned4(sinks)) || (dsinks && !aligned4(dsinks))) return FA_ERR_ALIGN;
   set_varlen(&a, cu_seqlens, total_rows);
   if (a.dq_slide) plan_slide(a, p->head_dim);  // size the units by the rows the batch holds
+  if (p->dtype != FA_DTYPE_F32) a.vl_kblocks = vl_kblocks(a);
   a.sink_logits = sinks;
   a.dsink = dsinks;
   const hipStream_t s = static_cast<hipStream_t>(stream);

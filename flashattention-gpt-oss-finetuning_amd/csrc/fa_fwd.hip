@@ -712,7 +712,9 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
 // computes.  LDS: 7 slots of K and V (8 KB each) and the mask patterns = 72 KB, two workgroups per
 // CU.  The per-half work is fwd_half, the same as fwd_kernel's.
 // ---------------------------------------------------------------------------------------------
-template <typename E>
+// VL: a packed batch's enumeration of the units (a separate instantiation, so that the
+// fixed-length kernel's code and registers are not touched by it).
+template <typename E, bool VL>
 __global__ __launch_bounds__(256, 2) void fwd_slide_kernel(const Args a) {
   constexpr int D = 64, HPW = 2, KS = D / 16, DB = D / 32;
   constexpr int TILE = 32 * D;    // one swizzled [32][D] tile of 16-bit values
@@ -729,14 +731,24 @@ __global__ __launch_bounds__(256, 2) void fwd_slide_kernel(const Args a) {
   const int r32 = lane & 31, hf = lane >> 5;
   const int W = a.W, S = a.S;
 
-  // unit -> (KV head, batch, head group, chunk), chunks fastest (as bwd_dq_slide_kernel)
+  // unit -> (KV head, batch, head group, chunk), chunks fastest (as bwd_dq_slide_kernel); a packed
+  // batch hands out only the chunks with rows: (KV head, head group), then each sequence's chunks
   const int hg_n = a.G / 8;
   const int unit = xcd_remap(blockIdx.x, gridDim.x);
-  const int chunk = unit % a.slide_ncu;
-  const int rest = unit / a.slide_ncu;
-  const int hg = rest % hg_n;
-  const int bk = rest / hg_n;
-  const int b = bk % a.B, kvh = bk / a.B;
+  int chunk, hg, b, kvh;
+  if constexpr (VL) {
+    const int grp = unit / a.vl_units;
+    hg = grp % hg_n;
+    kvh = grp / hg_n;
+    if (!varlen_nth(a, unit % a.vl_units, a.vl_units, 32, a.slide_ct, b, chunk)) return;
+  } else {
+    chunk = unit % a.slide_ncu;
+    const int rest = unit / a.slide_ncu;
+    hg = rest % hg_n;
+    const int bk = rest / hg_n;
+    b = bk % a.B;
+    kvh = bk / a.B;
+  }
   const Seq sq = seq_of(a, b);
   const int L = sq.L;
   const int n_qt = (L + 31) / 32;
@@ -860,8 +872,10 @@ __global__ __launch_bounds__(256, 2) void fwd_slide_kernel(const Args a) {
 
 template <typename E>
 static hipError_t launch_fwd_slide_e(const Args& a, hipStream_t stream) {
-  const dim3 grid(unsigned(a.B * a.Hkv * (a.G / 8) * a.slide_ncu)), block(256);
-  hipLaunchKernelGGL((fwd_slide_kernel<E>), grid, block, 0, stream, a);
+  const int per = a.vl_units ? a.vl_units : a.B * a.slide_ncu;  // units per (KV head, head group)
+  const dim3 grid(unsigned(a.Hkv * (a.G / 8) * per)), block(256);
+  if (a.vl_units) hipLaunchKernelGGL((fwd_slide_kernel<E, true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((fwd_slide_kernel<E, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 
