@@ -296,6 +296,7 @@ def reference_cases_measure(fa, dev, steps, warmup):
     for name, hkv in REFERENCE_CASES.items():
         c = dict(CONFIGS["c1"], Hkv=hkv)
         qq, kk, vv, dd = make_inputs(c, dev)
+        warm_clocks(fa, c, qq, kk, vv, dd, 0.1)  # the GPU idled while the inputs were drawn
         tt = time_steps(fa, c, qq, kk, vv, dd, steps, warmup)
         w = _mod("flops").Workload(c["B"], c["Hq"], c["Hkv"], c["L"], c["D"], c["W"], c["S"])
         out[name] = {"shape": f"B=1 Hq=16 Hkv={hkv} L=4096 D=16 W=256 S=4 fp16", **mode_figures(w, tt)}
@@ -309,6 +310,7 @@ def fp32_measure(fa, cfg, dev, steps, warmup):
     import torch
 
     q, k, v, do = (t.float() for t in make_inputs(cfg, dev))
+    warm_clocks(fa, cfg, q, k, v, do, 0.1)
     tt = time_steps(fa, cfg, q, k, v, do, steps, warmup)
     w = _mod("flops").Workload(cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["L"], cfg["D"], cfg["W"], cfg["S"], elem_bytes=4)
     figs = mode_figures(w, tt)
@@ -782,6 +784,7 @@ def main():
         # the README shape, whose autograd step is bound by host work: eager and graph-replayed
         c1 = CONFIGS["c1"]
         q1, k1, v1, do1 = make_inputs(c1, dev)
+        warm_clocks(fa, c1, q1, k1, v1, do1, 0.1)
         t1 = time_steps(fa, c1, q1, k1, v1, do1, args.steps, args.warmup)
         line["c1_step"] = {"workload": "c1: " + c1["name"] + ", fwd+bwd", "eager_ms_per_step": round(t1["fwdbwd_ms"], 4),
                            "graph": graph_step_measure(fa, c1, q1, k1, v1, do1, args.steps)}

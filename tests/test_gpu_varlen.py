@@ -108,6 +108,26 @@ def test_varlen_parity(gpu, cu, Hq, Hkv, D, W, S, dtype):
     run_varlen(cu, Hq, Hkv, D, W, S, dtype, seed=cu[-1] % 97 + D, with_naive=cu[-1] * Hq <= 1 << 16)
 
 
+def _many_sequences(n, seed, max_len):
+    import random
+
+    rng = random.Random(seed)
+    lens = [rng.choice([0, 1, rng.randint(2, 40), rng.randint(41, max_len)]) for _ in range(n)]
+    return [0] + list(__import__("itertools").accumulate(lens))
+
+
+@pytest.mark.parametrize("cu,Hq,Hkv,D,W,S,dtype", [
+    # more sequences than a wave's 64 lanes: the kernels' enumeration of the pieces the batch holds
+    # (a prefix sum over the sequences, 64 per round) runs several rounds; empty and one-row
+    # sequences on the sliding kernels (sink rows in the dQ kernel) and on the 64-key dK/dV kernel
+    pytest.param(_many_sequences(150, 7, 300), 8, 1, 64, 128, 4, BF, id="150-sequences-sliding"),
+    pytest.param(_many_sequences(130, 8, 200), 8, 1, 64, 48, 20, FP, id="130-sequences-sink-chunks"),
+    pytest.param(_many_sequences(70, 9, 500), 16, 2, 64, 160, 0, BF, id="70-sequences-G8-W160"),
+])
+def test_varlen_many_sequences(gpu, cu, Hq, Hkv, D, W, S, dtype):
+    run_varlen(cu, Hq, Hkv, D, W, S, dtype, seed=len(cu), with_naive=cu[-1] * Hq <= 1 << 16)
+
+
 def _random_varlen_cases(n=12, seed=777):
     """Packed batches drawn from a fixed seed: 1-6 sequences of 0-500 rows each (empty ones
     included), every head dim, groups 1-8, windows from 1 to full causal, 0-40 positional sinks,
