@@ -32,7 +32,7 @@ FA_ERR_LAUNCH = -8
 FA_ERR_OVERFLOW = -9
 FA_ERR_SCALE = -10
 FA_ERR_SCRATCH = -11
-FA_SCRATCH_BYTES = 128 << 20
+FA_SCRATCH_BYTES = 72 << 20
 
 # Every function the header declares; the tests check that the library exports each one.
 EXPORTS = (
