@@ -581,10 +581,16 @@ __device__ __forceinline__ void dkdv_products(const uint16_t* Qt, const uint16_t
 template <typename E, int D>
 __device__ void fold_sink_keys(int b, int kvh, int nk, const Seq& sq, float* smem);
 
-// 16-bit elements of the dK/dV kernel's LDS: NSTG stages of two items (Q and dO tiles, 32 rows,
-// and 128 elements of row statistics each), or the fp32 partials of the head-slot sum if larger.
-__host__ __device__ constexpr int dkdv_lds_elems(int D) {
-  const int stages = (D == 128 ? 3 : 4) * 2 * (2 * 32 * D + 128);
+// The dK/dV kernel's LDS stages (see its staging).  KVL (D = 64 only): the K and V tiles of the
+// workgroup's 64 keys sit in LDS as well, and the score products read their B operands from there
+// every step instead of holding them in 32 registers; with two stages that leaves 160 VGPRs and
+// 49 KB of LDS, three workgroups per CU instead of two.
+__host__ __device__ constexpr int dkdv_stages(int D, bool kvl) { return D == 128 ? 3 : kvl ? 2 : 4; }
+// 16-bit elements of the dK/dV kernel's LDS: the stages of two items each (Q and dO tiles, 32
+// rows, and 128 elements of row statistics per item) and with KVL the K/V tiles, or the fp32
+// partials of the head-slot sum if larger.
+__host__ __device__ constexpr int dkdv_lds_elems(int D, bool kvl) {
+  const int stages = dkdv_stages(D, kvl) * 2 * (2 * 32 * D + 128) + (kvl ? 4 * 32 * D : 0);
   const int red = 2 * 2 * 2 * (D >= 32 ? D / 32 : 1) * 16 * 64;
   return stages > red ? stages : red;
 }
@@ -592,22 +598,24 @@ __host__ __device__ constexpr int dkdv_lds_elems(int D) {
 // Does key block 0's workgroup fold the sink keys itself (dq_sink_mode; the sink keys' (key,
 // column) pairs fit one pass of 256 threads; the dQ kernel's run list and the chunk sums fit the
 // kernel's LDS)?  Otherwise bwd_sink_fold_kernel does it after the dK/dV kernel.
-__host__ __device__ inline bool dkdv_folds_in_kernel(const Args& a, int D) {
+__host__ __device__ inline bool dkdv_folds_in_kernel(const Args& a, int D, bool kvl) {
   return a.sink_dq && (a.S < kKvKeys ? a.S : kKvKeys) * D <= 256 &&
-         ((a.dq_wgs + 3) & ~3) + 4 * 256 <= dkdv_lds_elems(D) / 2;
+         ((a.dq_wgs + 3) & ~3) + 4 * 256 <= dkdv_lds_elems(D, kvl) / 2;
 }
 
-// D = 16 keeps four waves per SIMD (at most 128 VGPRs); the wider head dims need more registers.
-template <typename E, int D>
-__global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Args a) {
+// D = 16 keeps four waves per SIMD (at most 128 VGPRs), D = 64 with KVL three (168); the wider
+// head dims need more registers.
+template <typename E, int D, bool KVL = false>
+__global__ __launch_bounds__(256, D == 16 ? 4 : KVL ? 3 : 1) void bwd_dkdv_kernel(const Args a) {
   constexpr int KS = D / 16;
   constexpr int DB = D >= 32 ? D / 32 : 1;
   constexpr int TILE = 32 * D;               // 32 rows of Q or dO, swizzled row-major
   constexpr int SLOT = 2 * TILE + 128;       // Q, dO, then lse2[32] and -delta[32] as fp32
   constexpr int STAGE = 2 * SLOT;            // two items per step
-  constexpr int NSTG = D == 128 ? 3 : 4;     // LDS stages: see the staging below
+  constexpr int NSTG = dkdv_stages(D, KVL);  // LDS stages: see the staging below
+  static_assert(!KVL || D == 64, "K/V operands from LDS: D = 64 only");
   constexpr int CPR = D / 8;                 // 16-byte chunks per row
-  __shared__ __attribute__((aligned(16))) uint16_t lds[dkdv_lds_elems(D)];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[dkdv_lds_elems(D, KVL)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -667,9 +675,27 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   const bool wave_on = ks0 < L && (!is_chunk || ks0 < S);
   const int wqlo = is_chunk ? qlo : max(qlo, ks0), wqhi = qhi;
 
-  // K^T / V^T operands, waited for after the first DMA issues (load_kv_operands)
-  u32x4 kf[KS], vf[KS];
-  load_kv_operands<D>(a, b, kvh, sq, key, kf, vf);
+  // K^T / V^T operands, waited for after the first DMA issues (load_kv_operands), or (KVL) the
+  // workgroup's K and V tiles by DMA into LDS: wave w loads tile w (K of half 0, V of half 0, K of
+  // half 1, V of half 1), swizzled row-major like the Q / dO tiles
+  u32x4 kf[KVL ? 1 : KS], vf[KVL ? 1 : KS];
+  uint16_t* const kvl = lds + NSTG * STAGE;
+  if constexpr (KVL) {
+    const bool tv = wave & 1;
+    const int64_t rs = tv ? a.sv[2] : a.sk[2];
+    const rsrc_t r = tv ? make_rsrc(reinterpret_cast<const char*>(a.v) + 2 * slice_off(a.sv, b, kvh, sq.row), span_bytes(L, a.sv[2], D))
+                        : make_rsrc(reinterpret_cast<const char*>(a.k) + 2 * slice_off(a.sk, b, kvh, sq.row), span_bytes(L, a.sk[2], D));
+    const int k0 = kKvKeys * kblk + 32 * (wave >> 1);
+#pragma unroll
+    for (int p = 0; p < 32 * D * 2 / 1024; ++p) {
+      const int pos = 64 * p + lane, row = pos / CPR, col = (pos % CPR) ^ swz<D>(row);
+      buf_dma16(r, kvl + wave * TILE + 512 * p, uint32_t((int64_t(k0 + row) * rs + 8 * col) * 2));
+    }
+  } else {
+    load_kv_operands<D>(a, b, kvh, sq, key, kf, vf);
+  }
+  const uint16_t* const Kw = kvl + (2 * kh) * TILE;  // this wave's K and V tiles (KVL)
+  const uint16_t* const Vw = Kw + TILE;
   const float cs = a.qsign ? -a.c : a.c;  // exponent factor: scale log2(e), with its sign
 
   f32x16 dk[DB], dv[DB];
@@ -777,8 +803,13 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int a_off = swz_off<D>(r32, hf * (D / 2) + 8 * ks);
-      sacc = E::mfma(lds16(Qt + a_off), kf[ks], sacc);
-      dpacc = E::mfma(lds16(Dt + a_off), vf[ks], dpacc);
+      if constexpr (KVL) {
+        sacc = E::mfma(lds16(Qt + a_off), lds16(Kw + a_off), sacc);
+        dpacc = E::mfma(lds16(Dt + a_off), lds16(Vw + a_off), dpacc);
+      } else {
+        sacc = E::mfma(lds16(Qt + a_off), kf[ks], sacc);
+        dpacc = E::mfma(lds16(Dt + a_off), vf[ks], dpacc);
+      }
     }
   };
   // The rest of an item, from its score products and LDS stage `buf`: P = exp2(s c - lse2) and
@@ -823,7 +854,7 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   if (n_steps > 0) {
     // loads NSTG - 1 steps ahead; step s waits for its own
     for (int k = 0; k < NSTG - 1; ++k) issue(k);
-    kv_operands_ready(kf, vf);
+    if constexpr (!KVL) kv_operands_ready(kf, vf);
     int cp = 0, cur = 0, nxt = NSTG - 1;  // stage of step s, stage of step s + NSTG - 1
     for (int s = 0; s < n_steps; ++s) {
       wait_vm_lgkm0_barrier<(NSTG - 2) * PER>();  // step s landed everywhere
@@ -909,7 +940,7 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : 1) void bwd_dkdv_kernel(const Ar
   // dq_sink_mode with at most 256 (sink key, column) pairs: key block 0's workgroup folds its
   // sink keys (see fold_sink_keys); the barrier makes its own slot writes visible to all its
   // threads, and every thread is past its last read of the LDS that the fold reuses.
-  if (partial_block && !is_chunk && dkdv_folds_in_kernel(a, D)) {
+  if (partial_block && !is_chunk && dkdv_folds_in_kernel(a, D, KVL)) {
     __syncthreads();
     fold_sink_keys<E, D>(b, kvh, min(min(S, kKvKeys), L), sq, reinterpret_cast<float*>(lds));
   }
@@ -1502,6 +1533,17 @@ static bool dkdv4_eligible(const Args& a, int D) {
          int64_t(a.B) * a.Hkv * ((a.L + kKvKeys - 1) / kKvKeys) <= device_cus();
 }
 
+// The D = 64 dK/dV kernel with its K/V operands in LDS (three workgroups per CU instead of two)
+// pays on grids of many short workgroups: windows up to 512 keys and at least six workgroups per
+// CU.  Measured on MI355X (Hq = 64 or 32, D = 64): 4096 workgroups at W = 128 (L = 32768) 247
+// against 272 us, at W = 512 666 against 695 us; 2048 workgroups (B = 4, G = 4) 67 against 75 us.
+// With fewer workgroups the last, partly filled round of three per CU costs more than the extra
+// workgroup gains (1024 at W = 128: 69 against 64 us; 512: 37 against 35 us), and the long sweeps
+// of full causal attention are slower with the extra LDS reads (843 against 936 us).
+static bool dkdv_kvl_pays(const Args& a, int grid) {
+  return a.W <= 512 && grid >= 6 * device_cus();
+}
+
 template <typename E, int D>
 static hipError_t launch_dkdv_d(const Args& a, hipStream_t stream) {
   Args ad = a;
@@ -1517,15 +1559,21 @@ static hipError_t launch_dkdv_d(const Args& a, hipStream_t stream) {
       folded = dkdv4_folds_in_kernel(ad, D, dkdv4_lds_elems<D>());
     } else {
       const int per_kv = a.vl_kblocks ? a.vl_kblocks : a.B * a.n_kblocks;  // regular workgroups per KV head
-      hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), dim3(a.n_chunk_wgs + a.Hkv * per_kv), dim3(256), 0, stream, ad);
+      const int grid = a.n_chunk_wgs + a.Hkv * per_kv;
+      bool kvl = false;
+      if constexpr (D == 64) kvl = dkdv_kvl_pays(a, grid);
+      if constexpr (D == 64) {
+        if (kvl) hipLaunchKernelGGL((bwd_dkdv_kernel<E, D, true>), dim3(grid), dim3(256), 0, stream, ad);
+      }
+      if (!kvl) hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), dim3(grid), dim3(256), 0, stream, ad);
       e = hipGetLastError();
-      folded = dkdv_folds_in_kernel(ad, D);
+      folded = dkdv_folds_in_kernel(ad, D, kvl);
     }
   } else {
     const int per_kv = a.vl_kblocks ? a.vl_kblocks : a.B * a.n_kblocks;
     hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), dim3(a.n_chunk_wgs + a.Hkv * per_kv), dim3(256), 0, stream, ad);
     e = hipGetLastError();
-    folded = dkdv_folds_in_kernel(ad, D);
+    folded = dkdv_folds_in_kernel(ad, D, false);
   }
   // the sink keys are folded inside the dK/dV kernel or by a launch of their own
   if (e != hipSuccess || a.nsp == 0 || folded) return e;

@@ -222,6 +222,25 @@ def test_baseline_configs(gpu, cfg):
              cfg.pop("dtype"), seed=0, **cfg)
 
 
+# Grids of at least six 64-key workgroups per CU with windows up to 512 keys run the D = 64 dK/dV
+# kernel variant that keeps its K/V operands in LDS (three workgroups per CU); these shapes take it
+# (the rule: B * Hkv * ceil(L / 64) + chunk workgroups >= 6 * CUs, W <= 512), with the in-kernel
+# sink fold (S = 4), sink chunk workgroups and the fold launch (S = 20), and G = 1.
+KV_LDS_CASES = [
+    pytest.param(6, 16, 8, 2048, 64, 128, 4, BF, id="W128-S4-G2"),
+    pytest.param(6, 16, 8, 2048, 64, 100, 20, FP, id="W100-S20-chunks"),
+    pytest.param(3, 16, 16, 2048, 64, 512, 0, FP, id="W512-G1"),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,D,W,S,dtype", KV_LDS_CASES)
+def test_kv_operands_in_lds_path(gpu, B, Hq, Hkv, L, D, W, S, dtype):
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert B * Hkv * -(-L // 64) >= 6 * cus and W <= 512, "the shape no longer takes the K/V-in-LDS variant"
+    print(f"case B={B} Hq={Hq} Hkv={Hkv} L={L} D={D} W={W} S={S} {dtype}", flush=True)
+    run_case(B, Hq, Hkv, L, D, W, S, dtype, seed=W + S)
+
+
 def test_autograd_path_and_noncontiguous_inputs(gpu):
     """E10: through the autograd Function with a non-contiguous dO and q given as a transposed
     [B, L, H, D] view; gradients equal the direct C-ABI path bit for bit."""
@@ -290,6 +309,7 @@ DETERMINISM_CASES = [
     pytest.param(1, 16, 16, 2048, 16, 256, 4, FP, id="D16-G1"),
     pytest.param(1, 8, 2, 1500, 64, 64, 40, BF, id="S40-chunks-and-fold"),
     pytest.param(1, 4, 2, 600, 64, 100, 4, torch.float32, id="float32"),
+    pytest.param(6, 16, 8, 2048, 64, 128, 4, BF, id="dkdv-kv-operands-in-lds"),
 ]
 
 
