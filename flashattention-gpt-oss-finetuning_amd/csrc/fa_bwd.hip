@@ -959,10 +959,12 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : KVL ? 3 : 1) void bwd_dkdv_kerne
 // the step loop has no barrier.  At the end the four waves' sums are added in LDS in wave order.
 // The per-item mathematics is bwd_dkdv_kernel's.
 // ---------------------------------------------------------------------------------------------
-template <int D>
+template <int D, int NW = 4>
 __host__ __device__ constexpr int dkdv4_lds_elems() {
-  const int stages = 2 * 4 * (2 * 32 * D + 128);
-  const int red = 3 * 2 * (D >= 32 ? D / 32 : 1) * 16 * 64 * 2;  // fp32 partials of waves 1..3
+  const int stages = 2 * NW * (2 * 32 * D + 128);
+  // fp32 partials of the waves that hand theirs on in the first round of the wave sum (NW / 2
+  // of them; NW = 4: waves 1..3 in one round)
+  const int red = (NW == 4 ? 3 : NW / 2) * 2 * (D >= 32 ? D / 32 : 1) * 16 * 64 * 2;
   return stages > red ? stages : red;
 }
 
@@ -973,18 +975,18 @@ __host__ __device__ inline bool dkdv4_folds_in_kernel(const Args& a, int D, int 
          ((a.dq_wgs + 3) & ~3) + 4 * 256 <= lds_elems / 2;
 }
 
-template <typename E, int D>
-__global__ __launch_bounds__(256, D == 16 ? 3 : 2) void bwd_dkdv4_kernel(const Args a) {
+template <typename E, int D, int NW = 4>
+__global__ __launch_bounds__(64 * NW, NW == 16 ? 4 : D == 16 && NW == 4 ? 3 : 2) void bwd_dkdv4_kernel(const Args a) {
   constexpr int KS = D / 16;
   constexpr int DB = D >= 32 ? D / 32 : 1;
   constexpr int TILE = 32 * D;
   constexpr int SLOT = 2 * TILE + 128;  // Q, dO, then lse2[32] and -delta[32] as fp32
-  constexpr int STAGE = 4 * SLOT;       // one slot per wave
+  constexpr int STAGE = NW * SLOT;      // one slot per wave
   constexpr int CPR = D / 8;
   constexpr int IPT = 32 * D * 2 / 1024;  // DMA instructions per tile (1 KiB each)
   constexpr int PER = 2 * IPT + 1;        // loads per wave and step
   static_assert(PER <= 63, "vmcnt immediate");
-  constexpr int LDS_ELEMS = dkdv4_lds_elems<D>();
+  constexpr int LDS_ELEMS = dkdv4_lds_elems<D, NW>();
   __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];
 
   const int tid = threadIdx.x;
@@ -1019,7 +1021,7 @@ __global__ __launch_bounds__(256, D == 16 ? 3 : 2) void bwd_dkdv4_kernel(const A
   // steps: (head group g, row block qb), g outermost so that descriptors change once per group
   const int qb_lo = qlo / 32;
   const int n_qb = qhi > qlo ? (qhi + 31) / 32 - qb_lo : 0;
-  const int n_steps = (G / 4) * n_qb;
+  const int n_steps = (G / NW) * n_qb;
 
   // staging: this wave's Q and dO tiles (IPT instructions each, lane l of instruction p loading the
   // global chunk that the swizzle places at 16-byte position 64p + l) and its row statistics
@@ -1039,7 +1041,7 @@ __global__ __launch_bounds__(256, D == 16 ? 3 : 2) void bwd_dkdv4_kernel(const A
     const int g = s / n_qb, qb = qb_lo + s % n_qb;
     if (g != fg) {
       fg = g;
-      const int h = kvh * G + 4 * g + wave;
+      const int h = kvh * G + NW * g + wave;
       rq = make_rsrc(reinterpret_cast<const char*>(a.q) + 2 * slice_off(a.sq, b, h, sq.row), q_bytes);
       rd = make_rsrc(reinterpret_cast<const char*>(a.dout) + 2 * slice_off(a.sdo, b, h, sq.row), d_bytes);
       rs = make_rsrc(reinterpret_cast<const char*>(a.delta + (int64_t(b) * a.Hq + h) * nblk * 64), uint32_t(nblk * 256));
@@ -1118,30 +1120,45 @@ __global__ __launch_bounds__(256, D == 16 ? 3 : 2) void bwd_dkdv4_kernel(const A
     }
   }
 
-  // ---- add the four waves' sums (wave 0 gets waves 1..3's), fixed order ------------------------
+  // ---- add the waves' sums into wave 0, in a fixed order: with 4 waves, waves 1..3's in wave
+  // order; with more, pairwise in rounds (round r: wave w with w % 2r == r hands its sum to w - r)
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   float* red = reinterpret_cast<float*>(lds);
-  if (wave > 0) {
+  constexpr int RW = 2 * DB * 16 * 64;  // floats of one wave's sums
+  auto put = [&](int region) {
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        red[(((wave - 1) * 2 + 0) * DB * 16 + db * 16 + e) * 64 + lane] = dk[db][e];
-        red[(((wave - 1) * 2 + 1) * DB * 16 + db * 16 + e) * 64 + lane] = dv[db][e];
+        red[region * RW + ((0 * DB + db) * 16 + e) * 64 + lane] = dk[db][e];
+        red[region * RW + ((1 * DB + db) * 16 + e) * 64 + lane] = dv[db][e];
       }
-  }
-  __syncthreads();
-  if (wave == 0) {
+  };
+  auto add = [&](int region) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        dk[db][e] += red[region * RW + ((0 * DB + db) * 16 + e) * 64 + lane];
+        dv[db][e] += red[region * RW + ((1 * DB + db) * 16 + e) * 64 + lane];
+      }
+  };
+  if constexpr (NW == 4) {
+    if (wave > 0) put(wave - 1);
+    __syncthreads();
+    if (wave == 0) {
 #pragma unroll 1  // (one wave's sums at a time: unrolled, all 3 * 32 * DB loads are live at once)
-    for (int w = 0; w < 3; ++w)
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          dk[db][e] += red[((w * 2 + 0) * DB * 16 + db * 16 + e) * 64 + lane];
-          dv[db][e] += red[((w * 2 + 1) * DB * 16 + db * 16 + e) * 64 + lane];
-        }
+      for (int w = 0; w < 3; ++w) add(w);
+    }
+  } else {
+#pragma unroll 1
+    for (int r = 1; r < NW; r *= 2) {
+      if (wave % (2 * r) == r) put(wave / (2 * r));
+      __syncthreads();
+      if (wave % (2 * r) == 0) add(wave / (2 * r));
+      __syncthreads();  // (the regions are written again in the next round)
+    }
   }
 
   // ---- outputs: lane (key, hf) holds head-dim indices 32db + 16hf + e (D == 16: hf == 0) ------
@@ -1330,7 +1347,7 @@ __device__ void fold_sink_keys(int b, int kvh, int nk, const Seq& sq, float* sme
     const int nv = min(ncu, ((sq.L + 31) / 32 + Ak.slide_ct - 1) / Ak.slide_ct);
     const int base = (kvh * Ak.B + b) * hgn * ncu;
     nr = hgn * nv;
-    for (int i = t; i < nr; i += 256) runs[i] = base + (i / nv) * ncu + i % nv;
+    for (int i = t; i < nr && t < 256; i += 256) runs[i] = base + (i / nv) * ncu + i % nv;
   } else {
     constexpr int nx = 8;
     const int tpk = Ak.n_qtiles * (Ak.G / Ak.wh);
@@ -1342,7 +1359,7 @@ __device__ void fold_sink_keys(int b, int kvh, int nk, const Seq& sq, float* sme
       const int x_lo = x * per + min(x, rem), x_hi = x_lo + per + (x < rem ? 1 : 0);
       const int r_lo = max(x_lo, lo), r_hi = min(x_hi, hi);
       const int n = r_hi > r_lo ? min(wgs_x, r_hi - r_lo) : 0;
-      for (int i = t; i < n; i += 256) runs[nr + i] = r_lo + i;
+      for (int i = t; i < n && t < 256; i += 256) runs[nr + i] = r_lo + i;
       nr += n;
     }
   }
@@ -1544,6 +1561,17 @@ static bool dkdv_kvl_pays(const Args& a, int grid) {
   return a.W <= 512 && grid >= 6 * device_cus();
 }
 
+// Waves (query-head slots) per workgroup of bwd_dkdv4_kernel: its grid is at most two 32-key
+// workgroups per CU, so with a large KV group (an MQA layer, or a KV-group shard) four waves leave
+// SIMDs idle and each wave sweeps G / 4 heads.  Up to two waves per SIMD, the workgroup takes 8
+// waves (or 16 at D = 16, whose 122 VGPRs allow four per SIMD) when G is a multiple of that.
+static int dkdv4_waves(const Args& a, int D, int grid) {
+  const int waves = 8 * device_cus();  // two per SIMD
+  if (D == 16 && a.G % 16 == 0 && grid * 16 <= waves) return 16;
+  if (a.G % 8 == 0 && grid * 8 <= waves) return 8;
+  return 4;
+}
+
 template <typename E, int D>
 static hipError_t launch_dkdv_d(const Args& a, hipStream_t stream) {
   Args ad = a;
@@ -1554,9 +1582,22 @@ static hipError_t launch_dkdv_d(const Args& a, hipStream_t stream) {
   if constexpr (D <= 64) {
     if (dkdv4_eligible(a, D)) {
       ad.n_kblocks = (a.L + 31) / 32;  // 32-key blocks
-      hipLaunchKernelGGL((bwd_dkdv4_kernel<E, D>), dim3(a.B * a.Hkv * ad.n_kblocks), dim3(256), 0, stream, ad);
+      const int grid = a.B * a.Hkv * ad.n_kblocks;
+      const int nw = dkdv4_waves(a, D, grid);
+      if constexpr (D == 16) {
+        if (nw == 16) {
+          hipLaunchKernelGGL((bwd_dkdv4_kernel<E, D, 16>), dim3(grid), dim3(1024), 0, stream, ad);
+          folded = dkdv4_folds_in_kernel(ad, D, dkdv4_lds_elems<D, 16>());
+        }
+      }
+      if (nw == 8) {
+        hipLaunchKernelGGL((bwd_dkdv4_kernel<E, D, 8>), dim3(grid), dim3(512), 0, stream, ad);
+        folded = dkdv4_folds_in_kernel(ad, D, dkdv4_lds_elems<D, 8>());
+      } else if (nw == 4) {
+        hipLaunchKernelGGL((bwd_dkdv4_kernel<E, D>), dim3(grid), dim3(256), 0, stream, ad);
+        folded = dkdv4_folds_in_kernel(ad, D, dkdv4_lds_elems<D>());
+      }
       e = hipGetLastError();
-      folded = dkdv4_folds_in_kernel(ad, D, dkdv4_lds_elems<D>());
     } else {
       const int per_kv = a.vl_kblocks ? a.vl_kblocks : a.B * a.n_kblocks;  // regular workgroups per KV head
       const int grid = a.n_chunk_wgs + a.Hkv * per_kv;

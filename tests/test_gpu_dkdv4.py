@@ -4,6 +4,8 @@ and grids of 64-key blocks (B * Hkv * ceil(L / 64)) no larger than the CU count.
 
 The cases walk its edges:
   * D = 16, 32 and 64; G = 4, 8 and 16 (one, two and four steps of 4 heads per row block);
+  * workgroups of 8 and 16 waves (query-head slots), which small grids with G a multiple of 8 (or of
+    16 at D = 16) take: the shard-sized G = 8 layer and the reference's Hkv = 1 default case;
   * L = 1 and partial last blocks; W = 1, 33, 128 and 512 (its largest window);
   * sink keys in dq_sink_mode (S <= 16 with rows past key block 0's window: the dQ kernel takes
     those rows, and key block 0's workgroup folds the partials), and S = 40 with every row inside
@@ -34,6 +36,9 @@ DKDV4_CASES = [
     pytest.param(1, 8, 1, 2000, 64, 96, 12, BF, id="long-dq-sink"),
     pytest.param(1, 8, 2, 333, 16, 50, 3, FP, id="D16-G4"),
     pytest.param(2, 4, 1, 257, 32, 128, 0, BF, id="D32-B2"),
+    pytest.param(1, 8, 1, 4096, 64, 128, 4, BF, id="G8-8-waves-shard"),
+    pytest.param(1, 16, 1, 4096, 16, 256, 4, FP, id="G16-D16-16-waves-hkv1"),
+    pytest.param(2, 32, 2, 700, 16, 40, 0, FP, id="G16-D16-16-waves-B2"),
 ]
 
 
@@ -51,10 +56,13 @@ def test_dkdv4_learned_sinks(gpu):
 @pytest.mark.parametrize("cu,D,W,S,sinks", [
     ([0, 1, 130, 130, 600], 64, 128, 4, True),
     ([0, 300, 333, 1000], 32, 200, 0, False),
+    ([0, 17, 17, 900, 1900], 16, 128, 4, True),
 ])
 def test_dkdv4_varlen(gpu, cu, D, W, S, sinks):
     print(f"case varlen cu={cu} D={D} W={W} S={S} sinks={sinks}", flush=True)
-    run_varlen(cu, 8, 2, D, W, S, BF, seed=13, sinks=sinks)
+    # D = 16: a G = 16 group (16-wave workgroups); otherwise G = 4
+    Hq, Hkv = (16, 1) if D == 16 else (8, 2)
+    run_varlen(cu, Hq, Hkv, D, W, S, BF, seed=13, sinks=sinks)
 
 
 def _dkdv4_random_cases(n=16, seed=404):

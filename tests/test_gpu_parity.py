@@ -310,6 +310,8 @@ DETERMINISM_CASES = [
     pytest.param(1, 8, 2, 1500, 64, 64, 40, BF, id="S40-chunks-and-fold"),
     pytest.param(1, 4, 2, 600, 64, 100, 4, torch.float32, id="float32"),
     pytest.param(6, 16, 8, 2048, 64, 128, 4, BF, id="dkdv-kv-operands-in-lds"),
+    pytest.param(1, 16, 1, 4096, 16, 256, 4, FP, id="dkdv-32-key-16-waves"),
+    pytest.param(1, 8, 1, 4096, 64, 128, 4, BF, id="dkdv-32-key-8-waves"),
 ]
 
 
