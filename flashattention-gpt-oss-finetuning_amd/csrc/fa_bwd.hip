@@ -71,8 +71,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   // Small head dims (D <= 32): a key block's compute is short next to the latency of fetching the
   // next one, so (as in the forward) every block of a tile, up to NBUF at a time, is fetched at
   // once by LDS DMA into a buffer of its own and the blocks are then computed back to back; the
-  // first tile's rows come in the same round trip.  Wider heads double-buffer through registers.
+  // first tile's rows come in the same round trip.  Wider heads double-buffer (see KDMA).
   constexpr bool PRE = D <= 32;
+  // D = 64: key blocks by DMA into two buffers, one block ahead (16 registers fewer than staging
+  // them through registers; c3 dQ 867 -> 839 us).  D = 128 stages through registers, which
+  // measured the same or 0.5% faster there.
+  constexpr bool KDMA = D == 64;
   constexpr int NBUF = PRE ? 32768 / (2 * BUF) : 2;  // 32 KiB of K/V blocks
   __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF * BUF + 4 * STASH + PT_EXTRA];
 
@@ -209,8 +213,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
     // and lane l of instruction p (of K or V) loads the chunk that the swizzle places at position
     // 64 p + l (as the forward's)
     constexpr int IPT = CPB / 64;
-    constexpr int NIW = PRE ? 2 * IPT / 4 : 1;
-    static_assert(!PRE || (NIW >= 1 && 2 * IPT == 4 * NIW), "whole DMA instructions per wave");
+    constexpr int NIW = (PRE || KDMA) ? 2 * IPT / 4 : 1;
+    static_assert(!(PRE || KDMA) || (NIW >= 1 && 2 * IPT == 4 * NIW), "whole DMA instructions per wave");
     auto dma_block = [&](int kb, int j) {
 #pragma unroll
       for (int n = 0; n < NIW; ++n) {
@@ -431,6 +435,24 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
           if (SINK && g0 == 0 && j == 0) refill();
         }
         __syncthreads();  // before the buffers are refilled
+      }
+    } else if constexpr (KDMA) {
+      // block i in buffer i & 1; block i + 1's DMA is issued before block i computes (its buffer was
+      // last read by block i - 1, behind the barrier that ended it) and waited for after it.  The
+      // next tile's rows (refill, 3 KS + 1 loads) are issued after block 1's DMA and may stay in
+      // flight past block 0's wait; later waits find them landed.
+      if (plan.nb > 0) {
+        dma_block(qplan_block(plan, 0), 0);
+        wait_vm_lgkm0_barrier<0>();
+      }
+      for (int i = 0; i < plan.nb; ++i) {
+        const bool more = i + 1 < plan.nb;
+        if (more) dma_block(qplan_block(plan, i + 1), (i + 1) & 1);
+        if (!SINK && i == 0) refill();
+        compute_block(qplan_block(plan, i), lds + (i & 1) * BUF);
+        if (SINK && i == 0) refill();
+        if (i == 0 && has_next) wait_vm_lgkm0_barrier<3 * KS + 1>();
+        else wait_vm_lgkm0_barrier<0>();
       }
     } else {
       if (plan.nb > 0) {  // (a tile past its sequence's end, in a variable-length batch, has none)
