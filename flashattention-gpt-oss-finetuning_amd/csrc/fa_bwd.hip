@@ -971,14 +971,16 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : KVL ? 3 : 1) void bwd_dkdv_kerne
 // ---------------------------------------------------------------------------------------------
 // dK / dV with 32-key workgroups (bwd_dkdv4_kernel), for window shapes without chunked sink rows
 // and KV groups of a multiple of 4 query heads (launch_bwd_dkdv picks it; dkdv4_eligible).  A
-// workgroup owns the 32 keys [ks0, ks0 + 32) of one KV head; its 4 waves all hold those keys'
-// K^T / V^T fragments and dK/dV accumulators, and each takes one query head of every group of 4:
-// step (g, qb) is head 4g + wave, 32-row block qb.  Every wave therefore needs the same row blocks,
-// so no wave idles on a block only the other key half sees (bwd_dkdv_kernel's 2-tile steps leave
-// a quarter of its wave-steps idle at W = 128), and the rows of a 32-key half are fewer than those
-// of a 64-key block.  Each wave stages its own items -- its Q and dO tiles and row statistics -- by
-// DMA into its own slot of a 2-stage LDS ring, one step ahead, and waits only for its own loads:
-// the step loop has no barrier.  At the end the four waves' sums are added in LDS in wave order.
+// workgroup owns the 32 keys [ks0, ks0 + 32) of one KV head; its NW waves (4, or 8 / 16 for large
+// KV groups on small grids, dkdv4_waves) all hold those keys' K^T / V^T fragments and dK/dV
+// accumulators, and each takes one query head of every group of NW: step (g, qb) is head
+// NW g + wave, 32-row block qb.  Every wave therefore needs the same row blocks, so no wave idles on
+// a block only the other key half sees (bwd_dkdv_kernel's 2-tile steps leave a quarter of its
+// wave-steps idle at W = 128), and the rows of a 32-key half are fewer than those of a 64-key
+// block.  Each wave stages its own items -- its Q and dO tiles and row statistics -- by DMA into its
+// own slot of a 2-stage LDS ring, one step ahead, and waits only for its own loads: the step loop
+// has no barrier.  At the end the waves' sums are added in LDS in a fixed order (in wave order for
+// 4 waves, pairwise in rounds for more).
 // The per-item mathematics is bwd_dkdv_kernel's.
 // ---------------------------------------------------------------------------------------------
 template <int D, int NW = 4>
@@ -1578,7 +1580,7 @@ static bool dkdv4_eligible(const Args& a, int D) {
 // against 272 us, at W = 512 666 against 695 us; 2048 workgroups (B = 4, G = 4) 67 against 75 us.
 // With fewer workgroups the last, partly filled round of three per CU costs more than the extra
 // workgroup gains (1024 at W = 128: 69 against 64 us; 512: 37 against 35 us), and the long sweeps
-// of full causal attention are slower with the extra LDS reads (843 against 936 us).
+// of full causal attention are slower with the extra LDS reads (936 against 843 us at Hkv = 4).
 static bool dkdv_kvl_pays(const Args& a, int grid) {
   return a.W <= 512 && grid >= 6 * device_cus();
 }
