@@ -364,6 +364,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
           // dQ^T += K^T dS^T: K^T read transposed from the row-major K block, keys in the row
           // order of the dS^T C tile
           float p[16], ds[16];
+          // D = 64: P, dS and the dQ products at a higher issue priority than the score products
+          // of the other workgroup's wave on the SIMD (c3 dQ 864 -> 828 us; D = 128, one wave per
+          // SIMD, was 4% slower with it, D = 16 unchanged)
+          if constexpr (D == 64) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             p[e] = fast_exp2(fmaf(s[e], a.c, -lse2));
@@ -375,6 +379,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
             acc[db] = E::mfma(tr_frag_swz<D>(Kl, 32 * sb, 32 * db, D), d0, acc[db]);
             acc[db] = E::mfma(tr_frag_swz<D>(Kl, 32 * sb + 16, 32 * db, D), d1, acc[db]);
           }
+          if constexpr (D == 64) __builtin_amdgcn_s_setprio(0);
           if constexpr (SINK) {
             if (ks0 == 0 && sink_rows) {
               // P and dS of keys [0, 16) (registers 0..7: keys 4hf + 0..3 and 8 + 4hf + 0..3 of
