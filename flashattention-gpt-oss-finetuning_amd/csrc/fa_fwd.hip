@@ -288,6 +288,7 @@ __device__ __forceinline__ void fwd_block_pv8(const Args& a, const uint16_t* Kl,
 #pragma unroll
   for (int sb = 0; sb < 2; ++sb)
     if (need[sb]) half_scores<BF16, D, HPW, 2>(a, Kl + 32 * sb * (D / 2), kb + 32 * sb, qw, q, qf, pat, eo, s[sb]);
+  __builtin_amdgcn_s_setprio(1);  // (as fwd_half: the softmax and P V above the score products)
   // V^T operands, shared by the heads: lane (r, hf) byte 8m + t is V[16m + 8hf + t][32db + r].
   // Lane 2j + b of 16-lane group g addresses key 16m + 8(g / 2) + j, bytes 32db + 16(g % 2) + 8b.
   u32x4 vf[DB][2];
@@ -344,6 +345,7 @@ __device__ __forceinline__ void fwd_block_pv8(const Args& a, const uint16_t* Kl,
     const u32x4 ones = {0x38383838u, 0x38383838u, 0x38383838u, 0x38383838u};  // e4m3 1.0
     lacc[h] = mfma_fp8(ones, ones, plo, phi, lacc[h]);
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 
