@@ -372,9 +372,13 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   constexpr int STASH = kStash ? HPW * KS * 512 : 0;  // per wave: the next tile's Q fragments
   // Small head dims (16-bit D <= 32): a block's compute is short next to the latency of fetching
   // the next block, so every block of a tile (up to NBUF at a time) is fetched at once, by LDS DMA,
-  // into NBUF buffers, and the blocks are then computed back to back.  Wider heads double-buffer
-  // through registers, one block ahead.
+  // into NBUF buffers, and the blocks are then computed back to back.  Wider heads double-buffer,
+  // one block ahead (through registers, or by DMA: KDMA).
   constexpr bool PRE = !F8 && D <= 32;
+  // 16-bit D = 128: key blocks by DMA into the two buffers, one block ahead, instead of through
+  // registers (219 instead of 240 VGPRs; c5 forward 204.6 -> 195.2 us).  At D = 64 the same form
+  // measured 0.8-2.3% slower at full causal, so D = 64 keeps the register path.
+  constexpr bool KDMA = !F8 && D == 128;
   constexpr int NBUF = PRE ? 32768 / (2 * BUF) : 2;  // 32 KiB of K/V blocks
   __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF * BUF + 4 * STASH + 2 * kPatterns * kPatternFloats];
 
@@ -584,24 +588,24 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
     }
   };
 
-  if constexpr (PRE) {
-    // DMA of a 64-key block into buffer j: the block's K and V tiles are CPB 16-byte chunks each,
-    // 2 CPB / 64 instructions of 64 lanes; wave w issues instructions [w NIW, (w + 1) NIW), and lane
-    // l of instruction p (of K or V) loads the chunk that the swizzle places at position 64 p + l
-    constexpr int IPT = CPB / 64;       // instructions per tile (K or V)
-    constexpr int NIW = 2 * IPT / 4;    // per wave
-    static_assert(NIW >= 1 && 2 * IPT == 4 * NIW, "whole instructions per wave");
-    auto dma_block = [&](int kb, int j) {
+  // DMA of a 64-key block into buffer j: the block's K and V tiles are CPB 16-byte chunks each,
+  // 2 CPB / 64 instructions of 64 lanes; wave w issues instructions [w NIW, (w + 1) NIW), and lane
+  // l of instruction p (of K or V) loads the chunk that the swizzle places at position 64 p + l
+  constexpr int IPT = CPB / 64;       // instructions per tile (K or V)
+  constexpr int NIW = 2 * IPT / 4;    // per wave
+  static_assert(!(PRE || KDMA) || (NIW >= 1 && 2 * IPT == 4 * NIW), "whole instructions per wave");
+  auto dma_block = [&](int kb, int j) {
 #pragma unroll
-      for (int n = 0; n < NIW; ++n) {
-        const int ii = wave * NIW + n, is_v = ii >= IPT, pi = is_v ? ii - IPT : ii;
-        const int pos = 64 * pi + lane, row = pos / CPR, col = (pos % CPR) ^ swz<D>(row);
-        uint16_t* dst = lds + j * BUF + (is_v ? KBUF : 0) + 512 * pi;
-        const uint32_t off = uint32_t(int64_t(kb + row) * (is_v ? bv : bk)) + 16u * uint32_t(col);
-        if (is_v) buf_dma16(rv, dst, off);
-        else buf_dma16(rk, dst, off);
-      }
-    };
+    for (int n = 0; n < NIW; ++n) {
+      const int ii = wave * NIW + n, is_v = ii >= IPT, pi = is_v ? ii - IPT : ii;
+      const int pos = 64 * pi + lane, row = pos / CPR, col = (pos % CPR) ^ swz<D>(row);
+      uint16_t* dst = lds + j * BUF + (is_v ? KBUF : 0) + 512 * pi;
+      const uint32_t off = uint32_t(int64_t(kb + row) * (is_v ? bv : bk)) + 16u * uint32_t(col);
+      if (is_v) buf_dma16(rv, dst, off);
+      else buf_dma16(rk, dst, off);
+    }
+  };
+  if constexpr (PRE) {
     if (plan.nb == 0) {  // no key block: the Q rows are still read out of the stash
       if (kStash && tile == first_tile) {
         stash_rows(t);
@@ -630,6 +634,26 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
       }
       for (int j = 0; j < ng; ++j) compute_block(qplan_block(plan, g0 + j), j);
       __syncthreads();  // before the buffers are refilled
+    }
+  } else if constexpr (KDMA) {
+    // block i in buffer i & 1; block i + 1's DMA is issued before block i computes (its buffer was
+    // last read by block i - 1, behind the barrier that ended it) and waited for after it; the next
+    // tile's Q rows (HPW KS loads, issued after it in block 0) may stay in flight past that wait
+    if (plan.nb > 0) {
+      dma_block(qplan_block(plan, 0), 0);
+      wait_vm_lgkm0_barrier<0>();
+    }
+    for (int i = 0; i < plan.nb; ++i) {
+      const bool more = i + 1 < plan.nb;
+      if (more) dma_block(qplan_block(plan, i + 1), (i + 1) & 1);
+      const bool stash_now = kStash && i == 0 && has_next;
+      if (stash_now) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        stash_rows(decode(next_tile));
+      }
+      compute_block(qplan_block(plan, i), i & 1);
+      if (stash_now) wait_vm_lgkm0_barrier<HPW * KS>();
+      else wait_vm_lgkm0_barrier<0>();
     }
   } else {
     if (plan.nb > 0) {  // (a tile past its sequence's end, in a variable-length batch, has none)
