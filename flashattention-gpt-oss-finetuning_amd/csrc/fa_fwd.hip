@@ -375,10 +375,12 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
   // into NBUF buffers, and the blocks are then computed back to back.  Wider heads double-buffer,
   // one block ahead (through registers, or by DMA: KDMA).
   constexpr bool PRE = !F8 && D <= 32;
-  // 16-bit D = 128: key blocks by DMA into the two buffers, one block ahead, instead of through
-  // registers (219 instead of 240 VGPRs; c5 forward 204.6 -> 195.2 us).  At D = 64 the same form
-  // measured 0.8-2.3% slower at full causal, so D = 64 keeps the register path.
-  constexpr bool KDMA = !F8 && D == 128;
+  // 16-bit D = 128 and the fp8 P V path (e4m3 K and V kept as they are in LDS): key blocks by DMA
+  // into the two buffers, one block ahead, instead of through registers (D = 128: 219 instead of
+  // 240 VGPRs, c5 forward 204.6 -> 195.2 us; fa_fwd_fp8_pv c3 536 -> 514 us, c5 164 -> 158 us).
+  // At 16-bit D = 64 the same form measured 0.8-2.3% slower at full causal, so it keeps the
+  // register path, and so does fp8 Q K^T with 16-bit P V (its V is widened on the way to LDS).
+  constexpr bool KDMA = (!F8 && D == 128) || F8 == 2;
   constexpr int NBUF = PRE ? 32768 / (2 * BUF) : 2;  // 32 KiB of K/V blocks
   __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF * BUF + 4 * STASH + 2 * kPatterns * kPatternFloats];
 
@@ -598,7 +600,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const Args a) {
 #pragma unroll
     for (int n = 0; n < NIW; ++n) {
       const int ii = wave * NIW + n, is_v = ii >= IPT, pi = is_v ? ii - IPT : ii;
-      const int pos = 64 * pi + lane, row = pos / CPR, col = (pos % CPR) ^ swz<D>(row);
+      const int pos = 64 * pi + lane, row = pos / CPR, col = (pos % CPR) ^ swz<F8 ? D / 2 : D>(row);
       uint16_t* dst = lds + j * BUF + (is_v ? KBUF : 0) + 512 * pi;
       const uint32_t off = uint32_t(int64_t(kb + row) * (is_v ? bv : bk)) + 16u * uint32_t(col);
       if (is_v) buf_dma16(rv, dst, off);
