@@ -73,10 +73,15 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   // once by LDS DMA into a buffer of its own and the blocks are then computed back to back; the
   // first tile's rows come in the same round trip.  Wider heads double-buffer (see KDMA).
   constexpr bool PRE = D <= 32;
-  // D = 64: key blocks by DMA into two buffers, one block ahead (16 registers fewer than staging
-  // them through registers; c3 dQ 867 -> 839 us).  D = 128 stages through registers, which
-  // measured the same or 0.5% faster there.
-  constexpr bool KDMA = D == 64;
+  // D >= 64: key blocks by DMA into two buffers, one block ahead (16 registers fewer than staging
+  // them through registers at D = 64, 32 at D = 128; c3 dQ 867 -> 839 us).
+  constexpr bool KDMA = D >= 64;
+  // D = 128 with sink rows: the sink keys' accumulators are split over the 4 waves by head-dim
+  // columns (16 registers a wave instead of 64), each wave taking every wave's rows for its 32
+  // columns (sink_split below), which leaves the D = 128 key loop (see compute_block) the
+  // registers it needs without spilling to scratch memory.
+  constexpr bool SPLIT = SINK && D == 128;
+  constexpr int NSA = SPLIT ? D / 64 : D / 16;  // 16-column blocks of the sink accumulators per wave
   constexpr int NBUF = PRE ? 32768 / (2 * BUF) : 2;  // 32 KiB of K/V blocks
   __shared__ __attribute__((aligned(16))) uint16_t lds[NBUF * BUF + 4 * STASH + PT_EXTRA];
 
@@ -171,11 +176,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
   }
   const uint32_t bk = uint32_t(2 * a.sk[2]), bv = uint32_t(2 * a.sv[2]);  // bytes per key row
 
-  // sink accumulators: lane l holds key 4(l/16) + i, head-dim column 16 nb + l % 16
-  f32x4 dks[SINK ? NB16 : 1], dvs[SINK ? NB16 : 1];
+  // sink accumulators: lane l holds key 4(l/16) + i, head-dim column 16 nb + l % 16 (SPLIT: column
+  // 16 (NSA wave + nb) + l % 16)
+  f32x4 dks[SINK ? NSA : 1], dvs[SINK ? NSA : 1];
   if constexpr (SINK) {
 #pragma unroll
-    for (int nb = 0; nb < NB16; ++nb) {
+    for (int nb = 0; nb < NSA; ++nb) {
       dks[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
       dvs[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -312,10 +318,93 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
       }
     };
 
+    // The sink keys' dV_s += P^T dO and dK_s += dS^T Q of one wave's 32 rows: P and dS from the
+    // [32 rows][16 keys] tiles Pt / St, dO and Q from the stash tiles Dt / Qt, into the accumulators'
+    // NSA 16-column blocks starting at column block nb0.
+    auto sink_products = [&](const uint16_t* Pt, const uint16_t* St, const uint16_t* Qt, const uint16_t* Dt, int nb0) {
+      // A operands P^T / dS^T (16 keys x 32 rows): lane l gets key l % 16, rows 8(l/16) + 0..7, by
+      // two transposing reads of 4 rows each
+      const int g4 = lane >> 4, i16 = lane & 15;
+      const int pr = (8 * g4 + (i16 >> 2)) * 16 + 4 * (i16 & 3);
+      const u32x2 pa0 = ds_read_tr16(Pt + pr), pa1 = ds_read_tr16(Pt + pr + 64);
+      const u32x2 sa0 = ds_read_tr16(St + pr), sa1 = ds_read_tr16(St + pr + 64);
+      const u32x4 pa = {pa0[0], pa0[1], pa1[0], pa1[1]}, sa = {sa0[0], sa0[1], sa1[0], sa1[1]};
+#pragma unroll
+      for (int nb = 0; nb < NSA; ++nb) {
+        // B operands dO / Q (32 rows x 16 columns): lane l gets column 16 (nb0 + nb) + l % 16 of the
+        // same rows, read transposed from the stash tiles
+        const int rr = 8 * g4 + (i16 >> 2), cc = 16 * (nb0 + nb) + 4 * (i16 & 3);
+        const u32x2 db0 = ds_read_tr16(Dt + swz_off<D>(rr, cc)), db1 = ds_read_tr16(Dt + swz_off<D>(rr + 4, cc));
+        const u32x2 qb0 = ds_read_tr16(Qt + swz_off<D>(rr, cc)), qb1 = ds_read_tr16(Qt + swz_off<D>(rr + 4, cc));
+        dvs[nb] = E::mfma16(pa, u32x4{db0[0], db0[1], db1[0], db1[1]}, dvs[nb]);
+        dks[nb] = E::mfma16(sa, u32x4{qb0[0], qb0[1], qb1[0], qb1[1]}, dks[nb]);
+      }
+    };
+    // SPLIT, after key block 0 of a tile with sink rows (every wave, whatever its rows): once every
+    // wave has written its P / dS tiles, each wave adds the products of every wave's rows (in wave
+    // order) to its own NSA column blocks; the barrier after them precedes the refill of the stashes.
+    auto sink_split = [&]() {
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int qu = t.q0 + 32 * (u % a.wq);  // wave u's rows
+        if (qu < L && qu + 31 >= sink_row0) {
+          const uint16_t* su = lds + NBUF * BUF + u * STASH;
+          sink_products(su + 2 * TILE, su + 2 * TILE + 512, su, su + TILE, NSA * wave);
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    // does any wave of the tile have sink rows (the condition of sink_split, uniform over the
+    // workgroup)?
+    const bool tile_sink = SPLIT && t.q0 < L && t.q0 + 32 * a.wq - 1 >= sink_row0;
+
     // one key block [kb, kb + 64) from the K tile at Kl (V follows it)
     auto compute_block = [&](int kb, const uint16_t* Kl) {
       if (wave_active) {
         const uint16_t* Vl = Kl + BN * D;
+        if constexpr (D == 128) {
+          // One wave per SIMD: when both 32-key halves of the block are unmasked (and the sink path
+          // does not need the first half's P and dS), both halves' score products are issued before
+          // either half's elementwise work, in one basic block, so that the second half's products
+          // run under the first half's exponentials.  The same operations per accumulator, in the
+          // same order, as the loop below.  With the DMA staging, the split sink accumulators and
+          // the one-chain masked path: c5 dQ 388 -> 367 us, and 347 -> 319 us without sink keys.
+          if (tile_full(kb, qw, W, S) && tile_full(kb + 32, qw, W, S) && !(SINK && kb == 0 && sink_rows)) {
+            f32x16 s2[2], dp2[2];
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+              u32x4 kf[KS], vf[KS];
+#pragma unroll
+              for (int ks = 0; ks < KS; ++ks) {
+                const int off = swz_off<D>(32 * sb + r32, hf * (D / 2) + 8 * ks);
+                kf[ks] = *reinterpret_cast<const u32x4*>(Kl + off);
+                vf[ks] = *reinterpret_cast<const u32x4*>(Vl + off);
+              }
+              f32x16 d0;
+#pragma unroll
+              for (int e = 0; e < 16; ++e) d0[e] = ndelta;
+#pragma unroll
+              for (int ks = 0; ks < KS; ++ks) {
+                s2[sb] = E::mfma(kf[ks], qf[ks], ks == 0 ? f32x16{} : s2[sb]);
+                dp2[sb] = E::mfma(vf[ks], dof[ks], ks == 0 ? d0 : dp2[sb]);
+              }
+            }
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+              float ds[16];
+#pragma unroll
+              for (int e = 0; e < 16; ++e) ds[e] = fast_exp2(fmaf(s2[sb][e], a.c, -lse2)) * dp2[sb][e];
+              const u32x4 d0 = pack8<E>(ds), d1 = pack8<E>(ds + 8);
+#pragma unroll
+              for (int db = 0; db < DB; ++db) {
+                acc[db] = E::mfma(tr_frag_swz<D>(Kl, 32 * sb, 32 * db, D), d0, acc[db]);
+                acc[db] = E::mfma(tr_frag_swz<D>(Kl, 32 * sb + 16, 32 * db, D), d1, acc[db]);
+              }
+            }
+            return;
+          }
+        }
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
           const int ks0 = kb + 32 * sb;
@@ -341,7 +430,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
               dp = E::mfma(vf[ks], dof[ks], ks == 0 ? d0 : dp);
             }
           };
-          if (tile_full(ks0, qw, W, S)) {
+          // (D = 128: full blocks take the path above; here the mask's bias is formed for every
+          // tile -- 0 throughout when it is full -- so that one chain of score products is emitted
+          // and the K/V operands stay next to it)
+          if (D != 128 && tile_full(ks0, qw, W, S)) {
             qk(f32x16{});
           } else {
             f32x16 bias;
@@ -399,23 +491,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
                 *reinterpret_cast<u32x2*>(Pt + o) = u32x2{E::pack2(pz[4 * j], pz[4 * j + 1]), E::pack2(pz[4 * j + 2], pz[4 * j + 3])};
                 *reinterpret_cast<u32x2*>(St + o) = u32x2{E::pack2(dz[4 * j], dz[4 * j + 1]), E::pack2(dz[4 * j + 2], dz[4 * j + 3])};
               }
-              // A operands P^T / dS^T (16 keys x 32 rows): lane l gets key l % 16, rows
-              // 8(l/16) + 0..7, by two transposing reads of 4 rows each
-              const int g4 = lane >> 4, i16 = lane & 15;
-              const int pr = (8 * g4 + (i16 >> 2)) * 16 + 4 * (i16 & 3);
-              const u32x2 pa0 = ds_read_tr16(Pt + pr), pa1 = ds_read_tr16(Pt + pr + 64);
-              const u32x2 sa0 = ds_read_tr16(St + pr), sa1 = ds_read_tr16(St + pr + 64);
-              const u32x4 pa = {pa0[0], pa0[1], pa1[0], pa1[1]}, sa = {sa0[0], sa0[1], sa1[0], sa1[1]};
-#pragma unroll
-              for (int nb = 0; nb < NB16; ++nb) {
-                // B operands dO / Q (32 rows x 16 columns): lane l gets column 16 nb + l % 16 of
-                // the same rows, read transposed from the stash tiles
-                const int rr = 8 * g4 + (i16 >> 2), cc = 16 * nb + 4 * (i16 & 3);
-                const u32x2 db0 = ds_read_tr16(Ds + swz_off<D>(rr, cc)), db1 = ds_read_tr16(Ds + swz_off<D>(rr + 4, cc));
-                const u32x2 qb0 = ds_read_tr16(Qs + swz_off<D>(rr, cc)), qb1 = ds_read_tr16(Qs + swz_off<D>(rr + 4, cc));
-                dvs[nb] = E::mfma16(pa, u32x4{db0[0], db0[1], db1[0], db1[1]}, dvs[nb]);
-                dks[nb] = E::mfma16(sa, u32x4{qb0[0], qb0[1], qb1[0], qb1[1]}, dks[nb]);
-              }
+              if constexpr (!SPLIT) sink_products(Pt, St, Qs, Ds, 0);  // (SPLIT: in sink_split)
             }
           }
         }
@@ -455,6 +531,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
         if (more) dma_block(qplan_block(plan, i + 1), (i + 1) & 1);
         if (!SINK && i == 0) refill();
         compute_block(qplan_block(plan, i), lds + (i & 1) * BUF);
+        if (SPLIT && i == 0 && tile_sink && qplan_block(plan, 0) == 0) sink_split();
         if (SINK && i == 0) refill();
         if (i == 0 && has_next) wait_vm_lgkm0_barrier<3 * KS + 1>();
         else wait_vm_lgkm0_barrier<0>();
@@ -470,6 +547,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
         if (more) gload(qplan_block(plan, i + 1));
         if (!SINK && i == 0) refill();
         compute_block(qplan_block(plan, i), lds + (i & 1) * BUF);
+        if (SPLIT && i == 0 && tile_sink && qplan_block(plan, 0) == 0) sink_split();
         if (SINK && i == 0) refill();
         if (more) sstore((i + 1) & 1);
         __syncthreads();
@@ -504,7 +582,29 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
       // the runs of one XCD start at the first wgs_x tiles of its share of that (batch, KV head),
       // which is how bwd_sink_fold_kernel finds the slots.
       const bool flush = !has_next || next_tile / tiles_per_kv != tile / tiles_per_kv;
-      if (flush) {
+      if constexpr (SPLIT) {
+        // each wave holds the whole workgroup's sums for its own columns: written as they are
+        if (flush) {
+          KArgs& A = args_fresh();
+          const int sr = A.srows;
+          float* slot = A.dq_sink_part + int64_t(run_first) * (2 * sr * D);
+          run_first = next_tile;
+          const int g4 = lane >> 4, i16 = lane & 15;
+#pragma unroll
+          for (int nb = 0; nb < NSA; ++nb) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+              const int key = 4 * g4 + ii;
+              if (key < sr) {
+                slot[(0 * sr + key) * D + 16 * (NSA * wave + nb) + i16] = dks[nb][ii];
+                slot[(1 * sr + key) * D + 16 * (NSA * wave + nb) + i16] = dvs[nb][ii];
+              }
+            }
+            dks[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            dvs[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+      } else if (flush) {
         KArgs& A = args_fresh();
         const int sr = A.srows;
         float* red = reinterpret_cast<float*>(lds);

@@ -152,6 +152,10 @@ EDGE_CASES = [
     pytest.param(1, 4, 4, 700, 16, 40, 3, FP, id="dq-sinks-D16-G1"),
     pytest.param(1, 8, 2, 900, 32, 100, 16, BF, id="dq-sinks-D32-S16"),
     pytest.param(1, 8, 1, 600, 128, 50, 7, BF, id="dq-sinks-D128-G8"),
+    # D = 128 sums the sink keys' dK/dV over every wave's rows by head-dim columns: tiles of 4 and 2
+    # row blocks whose waves differ in having sink rows, and waves past the sequence's end
+    pytest.param(1, 2, 2, 333, 128, 40, 5, FP, id="dq-sinks-D128-G1"),
+    pytest.param(2, 4, 2, 517, 128, 100, 16, BF, id="dq-sinks-D128-G2-B2"),
     pytest.param(2, 6, 2, 500, 64, 20, 9, FP, id="dq-sinks-G3-B2"),
     pytest.param(1, 4, 2, 200, 64, 136, 2, BF, id="dq-sinks-one-row"),
     pytest.param(8, 64, 64, 200, 32, 10, 2, BF, id="dq-sinks-many-groups"),
