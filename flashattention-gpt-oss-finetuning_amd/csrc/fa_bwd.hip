@@ -968,7 +968,10 @@ __global__ __launch_bounds__(256, D == 16 ? 4 : KVL ? 3 : 1) void bwd_dkdv_kerne
     // workgroup's wave on the SIMD (as the forward's softmax): c3 1217 -> 1164 us, c2 34.5 -> 33.8
     // us; D = 16 and 128 measured no gain
     if constexpr (D == 64) __builtin_amdgcn_s_setprio(1);
-    if (full) elementwise(std::false_type{});
+    // D = 128 (one wave per SIMD): the mask is applied to every item (it keeps every element of a
+    // full one), so that the score products, the elementwise work and the dV/dK products form one
+    // basic block that the scheduler can interleave (c5 dK/dV 361 -> 355 us)
+    if (D != 128 && full) elementwise(std::false_type{});
     else elementwise(std::true_type{});
     const u32x4 pb[2] = {pack8<E>(p), pack8<E>(p + 8)};
     const u32x4 sb[2] = {pack8<E>(ds), pack8<E>(ds + 8)};
