@@ -50,7 +50,8 @@ namespace fa {
 // a per-wave LDS tile [32 rows][16 keys] to become the A operand, and dO / Q are read transposed
 // from the wave's row-major stash tiles.  The accumulators are summed over the workgroup's waves
 // and written once per run of tiles of one KV group (see the flush below), so the key-major
-// kernel needs no workgroups for those rows.
+// kernel needs no workgroups for those rows.  (D = 128: each wave accumulates every wave's rows
+// for a quarter of the head-dim columns instead; see SPLIT.)
 // ---------------------------------------------------------------------------------------------
 template <typename E, int D, bool SINK>
 __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(const Args a) {
