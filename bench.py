@@ -340,6 +340,8 @@ def fp32_measure(fa, cfg, dev, steps, warmup):
         rs = max(w.flops(mode) / 157.3e12, w.bytes(mode) / 8.0e12)
         figs[mode]["roofline_us"] = round(rs * 1e6, 2)
         figs[mode]["roofline_frac"] = round(rs / (figs[mode]["ms"] * 1e-3), 4)
+        if "event_ms" in figs[mode]:
+            figs[mode]["event_roofline_frac"] = round(rs / (figs[mode]["event_ms"] * 1e-3), 4)
     del q, k, v, do
     torch.cuda.empty_cache()
     return {"dtype": "fp32", "peak_tflops": 157.3, **figs}
