@@ -728,11 +728,12 @@ __host__ __device__ constexpr int dkdv_lds_elems(int D, bool kvl) {
   return stages > red ? stages : red;
 }
 
-// Does key block 0's workgroup fold the sink keys itself (dq_sink_mode; the sink keys' (key,
-// column) pairs fit one pass of 256 threads; the dQ kernel's run list and the chunk sums fit the
-// kernel's LDS)?  Otherwise bwd_sink_fold_kernel does it after the dK/dV kernel.
+// Does key block 0's workgroup fold the sink keys itself (dq_sink_mode; the dQ kernel's run list
+// and the chunk sums fit the kernel's LDS)?  Otherwise bwd_sink_fold_kernel does it after the
+// dK/dV kernel.  Up to 256 (sink key, column) pairs the workgroup's threads split the runs as well
+// (fold_sink_keys); up to 2048 each thread sums whole chunks of four columns over every run.
 __host__ __device__ inline bool dkdv_folds_in_kernel(const Args& a, int D, bool kvl) {
-  return a.sink_dq && (a.S < kKvKeys ? a.S : kKvKeys) * D <= 256 &&
+  return a.sink_dq && (a.S < kKvKeys ? a.S : kKvKeys) * D <= 2048 &&
          ((a.dq_wgs + 3) & ~3) + 4 * 256 <= dkdv_lds_elems(D, kvl) / 2;
 }
 
@@ -1463,11 +1464,12 @@ __device__ void fold_sink_key(int b, int kvh, int key, const Seq& sq, float (&pa
 
 // fold_sink_keys: the same sums for all nk sink keys at once, in key block 0's workgroup.  A slot's
 // 2 nk D values (dK rows, then dV rows) are C = nk D / 2 chunks of four floats; thread t < P C
-// (P = 256 / C >= 2 slot groups) takes chunk t % C of the slots at positions j, j + P, j + 2P, ...
+// (P = 256 / C slot groups) takes chunk t % C of the slots at positions j, j + P, j + 2P, ...
 // (j = t / C) of the list [own slot, the dQ kernel's run slots in (XCD, tile) order], kBatch
 // 16-byte loads in flight at a time; the P group sums of a chunk are then added in LDS in order
-// j = 0, 1, ....  `smem` is the kernel's LDS, free at this point (dq_wgs run indices, then the P C
-// chunk sums).
+// j = 0, 1, ....  With C > 256 (D = 128 and up to 16 sink keys) thread t takes the chunks t,
+// t + 256, ... over the whole list.  `smem` is the kernel's LDS, free at this point (dq_wgs run
+// indices, then the P C chunk sums).
 template <typename E, int D>
 __device__ void fold_sink_keys(int b, int kvh, int nk, const Seq& sq, float* smem) {
   KArgs& Ak = args_fresh();
@@ -1507,6 +1509,46 @@ __device__ void fold_sink_keys(int b, int kvh, int nk, const Seq& sq, float* sme
     }
   }
   __syncthreads();
+  // chunk c of the output (c < Q: dK, else dV): total tot, scaled and stored as 16-bit
+  auto store_chunk = [&](int cc, const f32x4& tot) {
+    const bool is_dk = cc < Q;
+    const int e = 4 * (is_dk ? cc : cc - Q), key = e / D, col = e % D;
+    const float m = is_dk ? Ak.scale : 1.f;
+    const u32x2 out = {E::pack2(tot[0] * m, tot[1] * m), E::pack2(tot[2] * m, tot[3] * m)};
+    char* base = reinterpret_cast<char*>(is_dk ? Ak.dk : Ak.dv);
+    const int64_t at = is_dk ? slice_off(Ak.sdk, b, kvh, sq.row + key) : slice_off(Ak.sdv, b, kvh, sq.row + key);
+    *reinterpret_cast<u32x2*>(base + 2 * (at + col)) = out;
+  };
+  if (C > 256) {
+    // more chunks than threads: each thread sums whole chunks, the workgroup's own slot first and
+    // then the runs in order
+    const int64_t blk = int64_t(b * Ak.Hkv + kvh) * Ak.nsp;
+    const float* own = Ak.partial + blk * (Ak.n_chunks + 1) * slot_stride;
+    for (int cc = t; cc < C; cc += 256) {
+      const int off = cc < Q ? 4 * cc : srd + 4 * (cc - Q);
+      f32x4 tot = *reinterpret_cast<const f32x4*>(own + off);
+      const float* dsrc = Ak.dq_sink_part + off;
+      for (int i0 = 0; i0 < nr; i0 += kBatch) {
+        f32x4 x[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const int i = i0 + u;
+          x[u] = *reinterpret_cast<const f32x4*>(dsrc + int64_t(runs[i < nr ? i : 0]) * slot_stride);
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          if (i0 + u < nr) {
+            tot[0] += x[u][0];
+            tot[1] += x[u][1];
+            tot[2] += x[u][2];
+            tot[3] += x[u][3];
+          }
+        }
+      }
+      store_chunk(cc, tot);
+    }
+    return;
+  }
   const int c = t % C, j = t / C;
   const int off = c < Q ? 4 * c : srd + 4 * (c - Q);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -1545,13 +1587,7 @@ __device__ void fold_sink_keys(int b, int kvh, int nk, const Seq& sq, float* sme
       tot[2] += v[2];
       tot[3] += v[3];
     }
-    const bool is_dk = t < Q;
-    const int e = 4 * (is_dk ? t : t - Q), key = e / D, col = e % D;
-    const float m = is_dk ? Ak.scale : 1.f;
-    const u32x2 out = {E::pack2(tot[0] * m, tot[1] * m), E::pack2(tot[2] * m, tot[3] * m)};
-    char* base = reinterpret_cast<char*>(is_dk ? Ak.dk : Ak.dv);
-    const int64_t at = is_dk ? slice_off(Ak.sdk, b, kvh, sq.row + key) : slice_off(Ak.sdv, b, kvh, sq.row + key);
-    *reinterpret_cast<u32x2*>(base + 2 * (at + col)) = out;
+    store_chunk(t, tot);
   }
 }
 
