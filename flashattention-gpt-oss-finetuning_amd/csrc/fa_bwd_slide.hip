@@ -82,6 +82,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
   const int qt1 = min(qt0 + a.slide_ct, n_qt);
   if (qt0 >= qt1) return;  // past the end of a short sequence (variable-length batches)
   const int h = kvh * a.G + hg * kSlideWaves + wave;  // this wave's query head
+  const float sink_logit = a.sink_logits ? a.sink_logits[h] : 0.f;  // (a scalar load, before any store)
 
   // ---- the wave's stash: rows of one tile of head h by DMA, as bwd_dq_kernel's stash_rows
   uint16_t* const stash = lds + wave * STASH;
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
       uint32_t so = st_off[p];
       asm volatile("" : "+v"(so));  // computed here: hoisted, the offsets of every part stay live
       const uint32_t row = uint32_t(32 * qt) + (so >> 16), col = so & 0xffffu;
-      buf_dma16(r, stash + part * TILE + 512 * p, (row * rs + col) * 2);
+      buf_dma16_asm(r, stash + part * TILE + 512 * p, (row * rs + col) * 2);
     }
   };
   auto stash_rows = [&](int qt) {
@@ -128,8 +129,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
     kv_off = uint32_t((int64_t(row) * kv_rs + 8 * col) * 2);
   }
   const uint32_t half_bytes = uint32_t(32 * kv_rs * 2);
+  // (Every DMA of this kernel is issued from inline assembly: the compiler would wait for DMAs of
+  // its own before each transposed LDS read, and wherever it waits for the LSE load; the explicit
+  // waits of the tile loop cover them.)
   auto load_half = [&](int j, int slot) {
-    buf_dma16(rkv, ring + slot * HALF + (kind_v ? TILE : 0) + 512 * (wave & 3), kv_off + uint32_t(j) * half_bytes);
+    buf_dma16_asm(rkv, ring + slot * HALF + (kind_v ? TILE : 0) + 512 * (wave & 3), kv_off + uint32_t(j) * half_bytes);
   };
 
   // sink accumulators (dq_sink_mode): lane l holds key 4(l/16) + i, head-dim column 16 nb + l % 16
@@ -166,8 +170,13 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
     // every wave's loads for this tile have landed (each waited for its own before its stores;
     // in the first tile, all but the window halves)
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    // the next tile's diagonal half, into the slot this tile does not use
+    // this tile's LSE (the compiler waits for its load here, which also waits for every load and
+    // store issued before it), then the next tile's diagonal half into the slot this tile does not
+    // use, and the next tile's LSE (a spare load of the last tile's in the last tile)
+    const float lse2 = q < L ? lse_next * kLog2e : __builtin_inff();
+    asm volatile("" ::"v"(lse2));  // (keeps that wait ahead of the DMA)
     if (has_next) load_half(qt + 1, (qt + 1) % kRing);
+    lse_next = load_lse(min(qt + 1, qt1 - 1));
 
     // row operands and statistics from the stash
     const uint16_t* Qs = stash;
@@ -184,7 +193,6 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
     }
     const float delta = sum_halves(dsum);
     const float ndelta = -delta;
-    const float lse2 = q < L ? lse_next * kLog2e : __builtin_inff();
 
     f32x16 acc[DB];
 #pragma unroll
@@ -192,7 +200,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
     // The next tile's rows, once this tile's have been read out of the stash (after the sink half
     // on the sink path, which also reads the stash), in three parts issued between the window
     // halves: issued at once, a wave's 3 KS DMA instructions stall it while the CU's load path
-    // takes the whole workgroup's 96 KB.  Part 2 also loads the next tile's LSE.
+    // takes the whole workgroup's 96 KB.
     int refilled = 0;  // parts issued
     auto refill_part = [&]() {
       if (has_next) {
@@ -202,10 +210,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
             stash_part(qt + 1, 0);
             break;
           case 1: stash_part(qt + 1, 1); break;
-          case 2:
-            stash_part(qt + 1, 2);
-            lse_next = load_lse(qt + 1);
-            break;
+          case 2: stash_part(qt + 1, 2); break;
           default: break;
         }
       }
@@ -338,10 +343,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
       }
     }
     if (qt == qt0) {
-      // the first tile's window halves (every wave's share): only the next tile's half, issued at
-      // the top of this tile, may still be in flight
-      if (has_next) wait_vm_lgkm0_barrier<1>();
-      else wait_vm_lgkm0_barrier<0>();
+      // the first tile's window halves (every wave's share): only the next tile's half and LSE,
+      // issued at the top of this tile, may still be in flight
+      if (has_next) wait_vm_lgkm0_barrier<2>();
+      else wait_vm_lgkm0_barrier<1>();
     }
     refill_part();
     {
@@ -353,7 +358,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_slide_kernel(const Args a) {
         st[32 + r32] = ndelta;
       }
       if (A.sink_logits) {
-        float v = q < L ? fast_exp2(A.sink_logits[h] * kLog2e - lse2) * delta : 0.f;
+        float v = q < L ? fast_exp2(fmaf(sink_logit, kLog2e, -lse2)) * delta : 0.f;
 #pragma unroll
         for (int mm = 16; mm >= 1; mm >>= 1) v += __shfl_xor(v, mm);
         if (lane == 0) A.dsink_part[(int64_t(b) * A.Hq + h) * (A.Lp / 32) + qt] = -v;

@@ -190,9 +190,20 @@ __device__ __forceinline__ float buf_ldf(rsrc_t r, uint32_t off) {
 // LDS DMA (buffer_load_dwordx4 ... lds): every lane loads 16 bytes at byte offset `off` of the
 // buffer, and lane l's bytes land at lds_dst + 16 l (lds_dst is wave-uniform).  Out-of-range
 // offsets land zeros.  Completion is counted by vmcnt like any load; an LDS read of the data
-// must wait for it explicitly (the compiler does not).  (Checked on hardware.)
+// must wait for it explicitly: the compiler's own waits for these DMAs (before every transposed
+// LDS read, which it cannot tell apart from the DMA's destination) are not placed for that.
+// (Checked on hardware.)
 __device__ __forceinline__ void buf_dma16(rsrc_t r, uint16_t* lds_dst, uint32_t off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds_dst), 16, off, 0, 0, 0);
+}
+// The same DMA issued from inline assembly, which the compiler does not see: it adds no wait for
+// it before transposed LDS reads, and where it waits for an earlier load into registers
+// (s_waitcnt vmcnt(n), counted from the loads it knows of) it does not wait for this one when it
+// was issued after a wait it cannot see.  Only for kernels whose every wait for it is explicit.
+// (M0 holds the LDS address; the s_nop covers the M0-write-to-LDS-DMA hazard.)
+__device__ __forceinline__ void buf_dma16_asm(rsrc_t r, uint16_t* lds_dst, uint32_t off) {
+  const uint32_t la = uint32_t(size_t((__attribute__((address_space(3))) uint16_t*)lds_dst));
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %2, %0, 0 offen lds" ::"s"(r), "{m0}"(la), "v"(off) : "memory");
 }
 // LDS DMA of 4 bytes per lane (buffer_load_dword ... lds): lane l's word lands at lds_dst + 4 l.
 __device__ __forceinline__ void buf_dma4(rsrc_t r, uint16_t* lds_dst, uint32_t off) {

@@ -823,20 +823,26 @@ __global__ __launch_bounds__(256, 2) void fwd_slide_kernel(const Args a) {
     kv_off[n] = uint32_t((int64_t(row) * (ii >= 4 ? svr : skr) + 8 * col) * 2);
   }
   const uint32_t hb_k = uint32_t(32 * skr * 2), hb_v = uint32_t(32 * svr * 2);
-  auto load_half = [&](int j, int slot) {
+  // (ASM: from inline assembly, not waited for by the compiler's waits for the Q loads)
+  auto load_half = [&](int j, int slot, auto asm_dma) {
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       const int ii = 2 * wave + n;
       uint16_t* dst = ring + slot * HALF + (ii >= 4 ? TILE : 0) + 512 * (ii & 3);
-      if (ii >= 4) buf_dma16(rv, dst, kv_off[n] + uint32_t(j) * hb_v);
-      else buf_dma16(rk, dst, kv_off[n] + uint32_t(j) * hb_k);
+      if constexpr (decltype(asm_dma)::value) {
+        if (ii >= 4) buf_dma16_asm(rv, dst, kv_off[n] + uint32_t(j) * hb_v);
+        else buf_dma16_asm(rk, dst, kv_off[n] + uint32_t(j) * hb_k);
+      } else {
+        if (ii >= 4) buf_dma16(rv, dst, kv_off[n] + uint32_t(j) * hb_v);
+        else buf_dma16(rk, dst, kv_off[n] + uint32_t(j) * hb_k);
+      }
     }
   };
 
   // prologue: the first tile's Q, the sink half and the first tile's window halves
   load_q(qt0);
-  if (S > 0) load_half(0, NR);
-  for (int j = slide_hlo(qt0, W); j <= qt0; ++j) load_half(j, j % NR);
+  if (S > 0) load_half(0, NR, std::false_type{});
+  for (int j = slide_hlo(qt0, W); j <= qt0; ++j) load_half(j, j % NR, std::false_type{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   for (int qt = qt0; qt < qt1; ++qt) {
@@ -845,13 +851,21 @@ __global__ __launch_bounds__(256, 2) void fwd_slide_kernel(const Args a) {
     // every wave's share of this tile's halves has landed (each waited for its own loads before
     // its O stores); in the first tile, the patterns are written
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (has_next) load_half(qt + 1, (qt + 1) % NR);
+    // this tile's Q rows, before the next tile's loads: the compiler's wait for the Q loads (already
+    // complete) must not also wait for the next half's DMA, which is therefore issued from inline
+    // assembly after the copy (the empty statements keep the copy ahead of it)
     u32x4 qf[HPW][KS];
 #pragma unroll
     for (int h = 0; h < HPW; ++h)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qf[h][ks] = qn[h][ks] ^ a.qsign;
-    if (has_next) load_q(qt + 1);
+      for (int ks = 0; ks < KS; ++ks) {
+        qf[h][ks] = qn[h][ks] ^ a.qsign;
+        asm volatile("" : "+v"(qf[h][ks]));
+      }
+    if (has_next) {
+      load_half(qt + 1, (qt + 1) % NR, std::true_type{});
+      load_q(qt + 1);
+    }
 
     float m2[HPW], lsum[HPW];
     f32x16 acc[HPW][DB];
