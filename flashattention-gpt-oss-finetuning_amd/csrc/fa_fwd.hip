@@ -823,7 +823,8 @@ __global__ __launch_bounds__(256, 2) void fwd_slide_kernel(const Args a) {
     kv_off[n] = uint32_t((int64_t(row) * (ii >= 4 ? svr : skr) + 8 * col) * 2);
   }
   const uint32_t hb_k = uint32_t(32 * skr * 2), hb_v = uint32_t(32 * svr * 2);
-  // (ASM: from inline assembly, not waited for by the compiler's waits for the Q loads)
+  // (asm_dma = std::true_type: issued from inline assembly, which the compiler's waits for the Q
+  // loads do not wait for)
   auto load_half = [&](int j, int slot, auto asm_dma) {
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
